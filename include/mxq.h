@@ -1,0 +1,136 @@
+/*
+ * mxq.h — C ABI of libmxq: the MLX affine group-quantized linear on MI355X
+ * (gfx950), written from scratch in HIP.
+ *
+ * Each entry point replaces one operation that the reference reaches through
+ * MLX-Swift (third-party mlx-swift 0.32.3, which wraps the mlx-c C API):
+ *
+ *   mxq_quantize          <- quantized(w, groupSize:, bits:)
+ *                            `model/minimax h3/tools/quantize_h3_g64.py:132`,
+ *                            `Packages/z-image-swift/Sources/ZImage/Weights.swift:31`
+ *   mxq_dequantize        <- dequantized(wq, scales:, biases:, groupSize:, bits:)
+ *                            `model/minimax h3/H3Common.swift:382-401`
+ *   mxq_quantized_matmul  <- quantizedMM / quantizedMatmul(x, w, scales:, biases:,
+ *                            transpose: true, groupSize:, bits:) plus the
+ *                            optional "+ bias" of QuantizedLinear / MfLinear
+ *                            `model/minimax h3/H3Common.swift:358-368`,
+ *                            `model/3模块/ltx2.5专属/gemma4文本-(ltx专属).swift:306-312`
+ *   mxq_qmm, mxq_qmv      <- the two halves of that op (large-M MFMA kernel,
+ *                            small-M GEMV kernel), callable directly
+ *   mxq_pack, mxq_unpack  <- the packed-code layout itself (no MLX-Swift
+ *                            function; the layout of `weight` in the triple
+ *                            `model/minimax h3/H3Common.swift:280-281, 389-394`)
+ *
+ * Conventions (mirroring mlx-c: int status, out-parameters, no exceptions):
+ *   - Every function returns MXQ_OK (0) or a negative MXQ_ERR_* code; the
+ *     message for the last error on the calling thread is mxq_last_error().
+ *   - All tensor pointers are DEVICE pointers, row-major and contiguous,
+ *     owned by the caller. Functions enqueue on `stream` (a hipStream_t;
+ *     NULL = the default stream) and return without synchronising.
+ *   - No function allocates device memory.
+ *   - Packed layout: for output row n, code k occupies bits [k*bits, k*bits+bits)
+ *     of the little-endian bitstream formed by wq[n, 0..K*bits/32).
+ *     scales, biases: [rows, K/group_size]; w = q*scale + bias.
+ *   - bits in {2,3,4,5,6,8}; group_size in {32,64,128}; K % group_size == 0.
+ *   - Pointers must be at least 4-byte aligned (MXQ_ERR_ALIGNMENT otherwise).
+ */
+#ifndef MXQ_H
+#define MXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXQ_ABI_VERSION 1
+
+/* status codes */
+#define MXQ_OK 0
+#define MXQ_ERR_INVALID (-1)     /* shapes, bits, group size or dtype rejected (mlx would throw) */
+#define MXQ_ERR_UNSUPPORTED (-2) /* valid mlx arguments this library does not implement */
+#define MXQ_ERR_ALIGNMENT (-3)   /* a pointer is not 4-byte aligned */
+#define MXQ_ERR_NULL (-4)        /* a required pointer is NULL */
+#define MXQ_ERR_HIP (-5)         /* the HIP runtime reported an error */
+
+/* element types */
+#define MXQ_FLOAT32 0
+#define MXQ_BFLOAT16 1
+
+/* quantizer modes */
+#define MXQ_MODE_MINMAX 0   /* scale=(max-min)/(2^bits-1), bias=min */
+#define MXQ_MODE_MLX_EDGE 1 /* mlx's sign-aware edge quantizer (as recalled) */
+
+/* Largest M served by the GEMV kernel when mxq_quantized_matmul dispatches. */
+#define MXQ_QMV_MAX_M 8
+
+typedef void* mxq_stream; /* hipStream_t */
+
+/* Quantize w [rows, cols] (w_dtype MXQ_FLOAT32 or MXQ_BFLOAT16) into
+ * wq uint32 [rows, cols*bits/32] and scales/biases [rows, cols/group_size]
+ * (sb_dtype MXQ_FLOAT32 or MXQ_BFLOAT16). Codes are computed from the fp32
+ * scale and bias; the stored scale/bias are then rounded to sb_dtype.
+ * Replaces `quantized(w, groupSize:, bits:)` (mlx `quantize`), reached in the
+ * reference at `model/minimax h3/tools/quantize_h3_g64.py:132`. */
+int mxq_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int group_size,
+                 int bits, int mode, uint32_t* wq, void* scales, void* biases,
+                 int sb_dtype, mxq_stream stream);
+
+/* out [rows, cols] (out_dtype MXQ_FLOAT32 or MXQ_BFLOAT16) = q*scale + bias,
+ * evaluated as one fp32 fused multiply-add, then rounded to out_dtype (RNE).
+ * Replaces `dequantized(...)` / MfLinear.dequantizedWeight
+ * (`model/minimax h3/H3Common.swift:382-401`, which is 4-bit only; this
+ * handles every supported width). */
+int mxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
+                   int64_t rows, int64_t cols, int group_size, int bits, void* out,
+                   int out_dtype, mxq_stream stream);
+
+/* Pack codes uint8 [rows, cols] (each < 2^bits) into wq uint32 [rows, cols*bits/32].
+ * Codes >= 2^bits are masked to their low `bits` bits. */
+int mxq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
+             mxq_stream stream);
+
+/* Unpack wq uint32 [rows, cols*bits/32] into codes uint8 [rows, cols]. */
+int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t* codes,
+               mxq_stream stream);
+
+/* y bf16 [M, N] = x bf16 [M, K] * dequant(wq, scales, biases)^T (+ bias bf16 [N]).
+ * scales/biases bf16 [N, K/group_size]; fp32 accumulation; bias may be NULL.
+ * transpose must be 1 (the only form the reference uses,
+ * `model/minimax h3/H3Common.swift:358-359`); transpose == 0 returns
+ * MXQ_ERR_UNSUPPORTED. M <= MXQ_QMV_MAX_M runs the GEMV kernel, larger M the
+ * MFMA kernel. M == 0 or N == 0 is a no-op. */
+int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                         const void* scales, const void* biases, int64_t N, int transpose,
+                         int group_size, int bits, const void* bias, void* y,
+                         mxq_stream stream);
+
+/* Large-M path only (bf16 MFMA, weights unpacked in registers). Any M >= 0. */
+int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
+            const void* biases, int64_t N, int group_size, int bits, const void* bias,
+            void* y, mxq_stream stream);
+
+/* Small-M path only (split-K GEMV, no MFMA). 0 <= M <= MXQ_QMV_MAX_M. */
+int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
+            const void* biases, int64_t N, int group_size, int bits, const void* bias,
+            void* y, mxq_stream stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mxq_last_error(void);
+
+/* Short name of a status code. */
+const char* mxq_status_string(int status);
+
+/* Blocks until all work on `stream` has finished; reports asynchronous kernel
+ * errors as MXQ_ERR_HIP. */
+int mxq_stream_synchronize(mxq_stream stream);
+
+/* MXQ_ABI_VERSION of the loaded library. */
+int mxq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXQ_H */

@@ -1,0 +1,212 @@
+"""ctypes binding of the CPU oracle (oracle/libmxq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker. The product (wuxianhuabu_amd)
+never imports this module.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmxq_oracle.so")
+
+_lib = None
+
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    L = ctypes.CDLL(LIB_PATH)
+    L.orc_version.restype = _int
+    L.orc_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.orc_splitmix64_next.restype = ctypes.c_uint64
+    L.orc_normal_f32.argtypes = [ctypes.c_uint64, _i64, ctypes.c_double, ctypes.c_double, _f32p]
+    L.orc_normal_bf16.argtypes = [ctypes.c_uint64, _i64, ctypes.c_double, ctypes.c_double, _u16p]
+    L.orc_bf16_rne.argtypes = [ctypes.c_float]
+    L.orc_bf16_rne.restype = ctypes.c_uint16
+    L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_bf16_to_f32.restype = ctypes.c_float
+    L.orc_bf16_to_f32_n.argtypes = [_u16p, _i64, _f32p]
+    L.orc_f32_to_bf16_n.argtypes = [_f32p, _i64, _u16p]
+    for name in ("orc_pack_bitwise", "orc_pack_words"):
+        getattr(L, name).argtypes = [_u8p, _i64, _i64, _int, _u32p]
+        getattr(L, name).restype = _int
+    L.orc_unpack.argtypes = [_u32p, _i64, _i64, _int, _u8p]
+    L.orc_unpack.restype = _int
+    L.orc_quantize.argtypes = [_f32p, _i64, _i64, _int, _int, _int, _u8p, _u32p, _u16p, _u16p,
+                               _f32p, _f32p]
+    L.orc_quantize.restype = _int
+    L.orc_dequantize.argtypes = [_u32p, _u16p, _u16p, _i64, _i64, _int, _int, _f32p, _u16p]
+    L.orc_dequantize.restype = _int
+    for name in ("orc_qmm_f64", "orc_qmm_f64_bf16w"):
+        getattr(L, name).argtypes = [_u16p, _i64, _i64, _u32p, _u16p, _u16p, _i64, _int, _int,
+                                     _vp, _vp, _i64, _int, _f64p]
+        getattr(L, name).restype = _int
+    L.orc_qmm_mlx_cpu.argtypes = [_u16p, _i64, _i64, _u32p, _u16p, _u16p, _i64, _int, _int,
+                                  _int, _vp, _i64, _int, _u16p]
+    L.orc_qmm_mlx_cpu.restype = _int
+    L.orc_gelu_tanh_bf16.argtypes = [_u16p, _i64, _u16p]
+    _lib = L
+    return L
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise ValueError(f"oracle {what} rejected its arguments")
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# ---- generator / bf16 ------------------------------------------------------
+def normal_f32(seed, n, mean=0.0, std=1.0):
+    out = np.empty(int(n), np.float32)
+    lib().orc_normal_f32(seed, n, mean, std, out)
+    return out
+
+
+def normal_bf16(seed, n, mean=0.0, std=1.0):
+    out = np.empty(int(n), np.uint16)
+    lib().orc_normal_bf16(seed, n, mean, std, out)
+    return out
+
+
+def bf16_rne(a):
+    a = _c(a, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_f32_to_bf16_n(a.reshape(-1), a.size, out.reshape(-1))
+    return out
+
+
+def bf16_to_f32(a):
+    a = _c(a, np.uint16)
+    out = np.empty(a.shape, np.float32)
+    lib().orc_bf16_to_f32_n(a.reshape(-1), a.size, out.reshape(-1))
+    return out
+
+
+# ---- layout ----------------------------------------------------------------
+def pack_bitwise(codes, bits):
+    codes = _c(codes, np.uint8)
+    N, K = codes.shape
+    wq = np.empty((N, K * bits // 32), np.uint32)
+    _check(lib().orc_pack_bitwise(codes, N, K, bits, wq), "pack_bitwise")
+    return wq
+
+
+def pack_words(codes, bits):
+    codes = _c(codes, np.uint8)
+    N, K = codes.shape
+    wq = np.empty((N, K * bits // 32), np.uint32)
+    _check(lib().orc_pack_words(codes, N, K, bits, wq), "pack_words")
+    return wq
+
+
+def unpack(wq, K, bits):
+    wq = _c(wq, np.uint32)
+    N = wq.shape[0]
+    codes = np.empty((N, K), np.uint8)
+    _check(lib().orc_unpack(wq, N, K, bits, codes), "unpack")
+    return codes
+
+
+# ---- quantizer / dequant -----------------------------------------------------
+def quantize(w, gs, bits, mode=0):
+    w = _c(w, np.float32)
+    N, K = w.shape
+    G = K // gs
+    out = {
+        "codes": np.empty((N, K), np.uint8),
+        "wq": np.empty((N, K * bits // 32), np.uint32),
+        "scales_bf16": np.empty((N, G), np.uint16),
+        "biases_bf16": np.empty((N, G), np.uint16),
+        "scales_f32": np.empty((N, G), np.float32),
+        "biases_f32": np.empty((N, G), np.float32),
+    }
+    _check(lib().orc_quantize(w, N, K, gs, bits, mode, out["codes"], out["wq"],
+                              out["scales_bf16"], out["biases_bf16"], out["scales_f32"],
+                              out["biases_f32"]), "quantize")
+    return out
+
+
+def dequantize(wq, scales, biases, K, gs, bits):
+    wq = _c(wq, np.uint32)
+    N = wq.shape[0]
+    f = np.empty((N, K), np.float32)
+    b = np.empty((N, K), np.uint16)
+    _check(lib().orc_dequantize(wq, _c(scales, np.uint16), _c(biases, np.uint16), N, K, gs,
+                                bits, f, b), "dequantize")
+    return f, b
+
+
+# ---- matmul references ---------------------------------------------------------
+def _rows_arg(rows):
+    if rows is None:
+        return None, 0, None
+    r = np.ascontiguousarray(rows, dtype=np.int64)
+    return r.ctypes.data_as(ctypes.c_void_p), len(r), r
+
+
+def _qmm64(fn, x, wq, scales, biases, gs, bits, bias, rows, threads):
+    x = _c(x, np.uint16)
+    wq = _c(wq, np.uint32)
+    M, K = x.shape
+    N = wq.shape[0]
+    rp, nr, keep = _rows_arg(rows)
+    nrows = M if rows is None else nr
+    y = np.empty((nrows, N), np.float64)
+    bias_keep = None if bias is None else _c(bias, np.uint16)
+    bp = None if bias_keep is None else bias_keep.ctypes.data_as(ctypes.c_void_p)
+    _check(fn(x, M, K, wq, _c(scales, np.uint16), _c(biases, np.uint16), N, gs, bits, bp, rp,
+              nr, threads, y), fn.__name__)
+    del keep
+    return y
+
+
+def qmm_f64(x, wq, scales, biases, gs, bits, bias=None, rows=None, threads=8):
+    return _qmm64(lib().orc_qmm_f64, x, wq, scales, biases, gs, bits, bias, rows, threads)
+
+
+def qmm_f64_bf16w(x, wq, scales, biases, gs, bits, bias=None, rows=None, threads=8):
+    return _qmm64(lib().orc_qmm_f64_bf16w, x, wq, scales, biases, gs, bits, bias, rows, threads)
+
+
+def qmm_mlx_cpu(x, wq, scales, biases, gs, bits, accum=0, rows=None, threads=1):
+    x = _c(x, np.uint16)
+    wq = _c(wq, np.uint32)
+    M, K = x.shape
+    N = wq.shape[0]
+    rp, nr, keep = _rows_arg(rows)
+    nrows = M if rows is None else nr
+    y = np.empty((nrows, N), np.uint16)
+    _check(lib().orc_qmm_mlx_cpu(x, M, K, wq, _c(scales, np.uint16), _c(biases, np.uint16), N,
+                                 gs, bits, accum, rp, nr, threads, y), "qmm_mlx_cpu")
+    del keep
+    return y
+
+
+def gelu_tanh_bf16(a):
+    a = _c(a, np.uint16)
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_gelu_tanh_bf16(a.reshape(-1), a.size, out.reshape(-1))
+    return out

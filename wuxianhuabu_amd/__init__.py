@@ -1,0 +1,22 @@
+"""wuxianhuabu_amd — MI355X-native MLX affine group-quantized linear.
+
+The quantized-linear hot path of the reference's MLX-Swift DiT backbones,
+rebuilt in HIP for gfx950 behind the same operator surface:
+
+    quantized, dequantized, quantized_matmul (quantizedMatmul / quantizedMM),
+    QuantizedLinear, MfLinear
+
+Device memory and streams come from torch; every kernel lives in libmxq.so,
+whose C ABI is include/mxq.h.
+"""
+from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
+from .nn import MfLinear, QuantizedLinear  # noqa: F401
+from .ops import (dequantized, pack, quantized, quantized_matmul,  # noqa: F401
+                  quantizedMatmul, quantizedMM, unpack)
+from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
+
+__all__ = [
+    "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
+    "pack", "unpack", "QuantizedLinear", "MfLinear", "get_quantized", "infer_geometry",
+    "header_candidates", "lib", "LIB_PATH", "MXQError",
+]

@@ -1,0 +1,252 @@
+// mxq_api.cpp — the C ABI declared in include/mxq.h.
+//
+// Argument checking mirrors what mlx rejects before it launches anything
+// (unsupported bits / group size, K not a multiple of the group size, shape
+// mismatches between the packed weight and scales/biases), and each message
+// names the mlx operation it stands in for, as mlx's own messages do
+// ("[quantize] ...", "[quantized_matmul] ..."). The reference reaches these
+// checks through MLX-Swift (`model/minimax h3/H3Common.swift:358-359`).
+// Nothing here allocates device memory.
+#include "../../include/mxq.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "mxq_internal.hpp"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return MXQ_OK;
+}
+
+bool bits_supported(int bits) {
+  return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+}
+bool gs_supported(int gs) { return gs == 32 || gs == 64 || gs == 128; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+int check_bits_gs(const char* op, int bits, int gs, int64_t cols) {
+  if (!bits_supported(bits))
+    return fail(MXQ_ERR_INVALID,
+                "[%s] The requested number of bits %d is not supported. The supported "
+                "bits are 2, 3, 4, 5, 6 and 8.",
+                op, bits);
+  if (!gs_supported(gs))
+    return fail(MXQ_ERR_INVALID,
+                "[%s] The requested group size %d is not supported. The supported group "
+                "sizes are 32, 64, and 128.",
+                op, gs);
+  if (cols < 0 || cols % gs != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[%s] The last dimension of the matrix needs to be divisible by the "
+                "quantization group size %d. However the provided matrix has last "
+                "dimension %lld.",
+                op, gs, static_cast<long long>(cols));
+  return MXQ_OK;
+}
+
+int hip_status(const char* op, hipError_t e) {
+  if (e == hipSuccess) return ok();
+  return fail(MXQ_ERR_HIP, "[%s] HIP error: %s", op, hipGetErrorString(e));
+}
+
+bool dtype_ok(int d) { return d == MXQ_FLOAT32 || d == MXQ_BFLOAT16; }
+
+int check_matmul(const char* op, const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                 const void* scales, const void* biases, int64_t N, int gs, int bits,
+                 const void* bias, const void* y) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(MXQ_ERR_INVALID, "[%s] Negative dimension (M=%lld, N=%lld, K=%lld).", op,
+                static_cast<long long>(M), static_cast<long long>(N),
+                static_cast<long long>(K));
+  int rc = check_bits_gs(op, bits, gs, K);
+  if (rc) return rc;
+  if (K == 0)
+    return fail(MXQ_ERR_INVALID, "[%s] K must be positive (got 0).", op);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MXQ_ERR_INVALID, "[%s] Dimensions above 2^31-1 are not supported.", op);
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (!x || !wq || !scales || !biases || !y)
+    return fail(MXQ_ERR_NULL, "[%s] x, w, scales, biases and y must be non-NULL.", op);
+  if (!aligned4(x) || !aligned4(wq) || !aligned4(y) || !aligned4(scales) ||
+      !aligned4(biases) || (bias && !aligned4(bias)))
+    return fail(MXQ_ERR_ALIGNMENT, "[%s] All tensor pointers must be 4-byte aligned.", op);
+  return MXQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mxq_abi_version(void) { return MXQ_ABI_VERSION; }
+
+const char* mxq_last_error(void) { return g_last_error; }
+
+const char* mxq_status_string(int status) {
+  switch (status) {
+    case MXQ_OK: return "MXQ_OK";
+    case MXQ_ERR_INVALID: return "MXQ_ERR_INVALID";
+    case MXQ_ERR_UNSUPPORTED: return "MXQ_ERR_UNSUPPORTED";
+    case MXQ_ERR_ALIGNMENT: return "MXQ_ERR_ALIGNMENT";
+    case MXQ_ERR_NULL: return "MXQ_ERR_NULL";
+    case MXQ_ERR_HIP: return "MXQ_ERR_HIP";
+    default: return "MXQ_ERR_UNKNOWN";
+  }
+}
+
+int mxq_stream_synchronize(mxq_stream stream) {
+  return hip_status("synchronize", hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+}
+
+int mxq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
+             mxq_stream stream) {
+  if (!bits_supported(bits))
+    return fail(MXQ_ERR_INVALID, "[pack] The requested number of bits %d is not supported.",
+                bits);
+  if (rows < 0 || cols < 0 || (cols * bits) % 32 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[pack] cols*bits must be a non-negative multiple of 32 (rows=%lld, "
+                "cols=%lld, bits=%d).",
+                static_cast<long long>(rows), static_cast<long long>(cols), bits);
+  if (rows == 0 || cols == 0) return ok();
+  if (!codes || !wq) return fail(MXQ_ERR_NULL, "[pack] codes and wq must be non-NULL.");
+  if (!aligned4(wq)) return fail(MXQ_ERR_ALIGNMENT, "[pack] wq must be 4-byte aligned.");
+  return hip_status("pack", mxq::detail::launch_pack(codes, rows, cols, bits, wq,
+                                                     static_cast<hipStream_t>(stream)));
+}
+
+int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t* codes,
+               mxq_stream stream) {
+  if (!bits_supported(bits))
+    return fail(MXQ_ERR_INVALID, "[unpack] The requested number of bits %d is not supported.",
+                bits);
+  if (rows < 0 || cols < 0 || (cols * bits) % 32 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[unpack] cols*bits must be a non-negative multiple of 32 (rows=%lld, "
+                "cols=%lld, bits=%d).",
+                static_cast<long long>(rows), static_cast<long long>(cols), bits);
+  if (rows == 0 || cols == 0) return ok();
+  if (!codes || !wq) return fail(MXQ_ERR_NULL, "[unpack] codes and wq must be non-NULL.");
+  if (!aligned4(wq)) return fail(MXQ_ERR_ALIGNMENT, "[unpack] wq must be 4-byte aligned.");
+  return hip_status("unpack", mxq::detail::launch_unpack(wq, rows, cols, bits, codes,
+                                                         static_cast<hipStream_t>(stream)));
+}
+
+int mxq_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int group_size,
+                 int bits, int mode, uint32_t* wq, void* scales, void* biases, int sb_dtype,
+                 mxq_stream stream) {
+  int rc = check_bits_gs("quantize", bits, group_size, cols);
+  if (rc) return rc;
+  if (rows < 0) return fail(MXQ_ERR_INVALID, "[quantize] rows must be non-negative.");
+  if (!dtype_ok(w_dtype) || !dtype_ok(sb_dtype))
+    return fail(MXQ_ERR_INVALID,
+                "[quantize] Only float32 and bfloat16 weights, scales and biases are "
+                "supported.");
+  if (mode != MXQ_MODE_MINMAX && mode != MXQ_MODE_MLX_EDGE)
+    return fail(MXQ_ERR_INVALID, "[quantize] Unknown quantization mode %d.", mode);
+  if (rows == 0 || cols == 0) return ok();
+  if (!w || !wq || !scales || !biases)
+    return fail(MXQ_ERR_NULL, "[quantize] w, wq, scales and biases must be non-NULL.");
+  if (!aligned4(w) || !aligned4(wq) || !aligned4(scales) || !aligned4(biases))
+    return fail(MXQ_ERR_ALIGNMENT, "[quantize] All tensor pointers must be 4-byte aligned.");
+  return hip_status("quantize",
+                    mxq::detail::launch_quantize(w, w_dtype, rows, cols, group_size, bits, mode,
+                                                 wq, scales, biases, sb_dtype,
+                                                 static_cast<hipStream_t>(stream)));
+}
+
+int mxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
+                   int64_t rows, int64_t cols, int group_size, int bits, void* out,
+                   int out_dtype, mxq_stream stream) {
+  int rc = check_bits_gs("dequantize", bits, group_size, cols);
+  if (rc) return rc;
+  if (rows < 0) return fail(MXQ_ERR_INVALID, "[dequantize] rows must be non-negative.");
+  if (!dtype_ok(sb_dtype) || !dtype_ok(out_dtype))
+    return fail(MXQ_ERR_INVALID,
+                "[dequantize] Only float32 and bfloat16 scales, biases and outputs are "
+                "supported.");
+  if (rows == 0 || cols == 0) return ok();
+  if (!wq || !scales || !biases || !out)
+    return fail(MXQ_ERR_NULL, "[dequantize] w, scales, biases and out must be non-NULL.");
+  if (!aligned4(wq) || !aligned4(scales) || !aligned4(biases) || !aligned4(out))
+    return fail(MXQ_ERR_ALIGNMENT, "[dequantize] All tensor pointers must be 4-byte aligned.");
+  return hip_status("dequantize",
+                    mxq::detail::launch_dequantize(wq, scales, biases, sb_dtype, rows, cols,
+                                                   group_size, bits, out, out_dtype,
+                                                   static_cast<hipStream_t>(stream)));
+}
+
+int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
+            const void* biases, int64_t N, int group_size, int bits, const void* bias, void* y,
+            mxq_stream stream) {
+  int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
+                        bias, y);
+  if (rc) return rc;
+  if (M > MXQ_QMV_MAX_M)
+    return fail(MXQ_ERR_INVALID, "[qmv] M=%lld exceeds the GEMV limit %d.",
+                static_cast<long long>(M), MXQ_QMV_MAX_M);
+  if (M == 0 || N == 0) return ok();
+  return hip_status(
+      "quantized_matmul",
+      mxq::detail::launch_qmv(static_cast<const uint16_t*>(x), static_cast<int>(M),
+                              static_cast<int>(K), wq, static_cast<const uint16_t*>(scales),
+                              static_cast<const uint16_t*>(biases), static_cast<int>(N),
+                              group_size, bits, static_cast<const uint16_t*>(bias),
+                              static_cast<uint16_t*>(y), static_cast<hipStream_t>(stream)));
+}
+
+int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
+            const void* biases, int64_t N, int group_size, int bits, const void* bias, void* y,
+            mxq_stream stream) {
+  int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
+                        bias, y);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return ok();
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* xb = static_cast<const uint16_t*>(x);
+  const auto* sc = static_cast<const uint16_t*>(scales);
+  const auto* bi = static_cast<const uint16_t*>(biases);
+  const auto* bs = static_cast<const uint16_t*>(bias);
+  auto* yb = static_cast<uint16_t*>(y);
+  if (!mxq::detail::qmm_supports_bits(bits)) {
+    // 3- and 5-bit codes: the GEMV kernel handles any M in blocks of 8 rows.
+    return hip_status("quantized_matmul",
+                      mxq::detail::launch_qmv(xb, static_cast<int>(M), static_cast<int>(K), wq,
+                                              sc, bi, static_cast<int>(N), group_size, bits,
+                                              bs, yb, s));
+  }
+  return hip_status("quantized_matmul",
+                    mxq::detail::launch_qmm(xb, static_cast<int>(M), static_cast<int>(K), wq, sc,
+                                            bi, static_cast<int>(N), group_size, bits, bs, yb,
+                                            s));
+}
+
+int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                         const void* scales, const void* biases, int64_t N, int transpose,
+                         int group_size, int bits, const void* bias, void* y,
+                         mxq_stream stream) {
+  if (transpose != 1)
+    return fail(MXQ_ERR_UNSUPPORTED,
+                "[quantized_matmul] transpose=false (x * W with W stored [K, N]) is not "
+                "implemented; the quantized linear layers use transpose=true.");
+  if (M <= MXQ_QMV_MAX_M)
+    return mxq_qmv(x, M, K, wq, scales, biases, N, group_size, bits, bias, y, stream);
+  return mxq_qmm(x, M, K, wq, scales, biases, N, group_size, bits, bias, y, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,37 @@
+// mxq_internal.hpp — launchers behind the C ABI. Arguments are validated by
+// mxq_api.cpp before any of these is called; launchers only pick a kernel
+// instantiation and enqueue it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxq {
+namespace detail {
+
+hipError_t launch_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
+                       hipStream_t s);
+hipError_t launch_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits,
+                         uint8_t* codes, hipStream_t s);
+hipError_t launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int gs,
+                           int bits, int mode, uint32_t* wq, void* scales, void* biases,
+                           int sb_dtype, hipStream_t s);
+hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                             int sb_dtype, int64_t rows, int64_t cols, int gs, int bits,
+                             void* out, int out_dtype, hipStream_t s);
+
+// y[M,N] = x[M,K] * W^T (+ bias): small-M split-K GEMV (any M; rows of x are
+// processed in blocks of up to 8).
+hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,
+                      const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
+                      const uint16_t* bias, uint16_t* y, hipStream_t s);
+
+// Large-M bf16 MFMA kernel. Returns hipErrorNotSupported for widths it does
+// not implement (the caller then falls back to launch_qmv).
+hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,
+                      const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
+                      const uint16_t* bias, uint16_t* y, hipStream_t s);
+bool qmm_supports_bits(int bits);
+
+}  // namespace detail
+}  // namespace mxq

@@ -1,0 +1,276 @@
+// mxq_layout.hip — packer, unpacker, quantizer and dequantizer for the MLX
+// affine layout (gfx950). These run at load time, not in the sampling loop;
+// they are written for bit-exactness first and are HBM-bound.
+//
+// Reference behaviour:
+//   quantize   : mx.quantize(w, group_size=64, bits=4) in
+//                `model/minimax h3/tools/quantize_h3_g64.py:132`, and
+//                quantize(model:) in `Packages/z-image-swift/Sources/ZImage/Weights.swift:31`
+//   dequantize : MfLinear.dequantizedWeight, `model/minimax h3/H3Common.swift:382-401`
+//                (w = q*scale + bias in fp32, then bf16)
+//   layout     : `model/3模块/模型加载-通用.swift:178-185` (shape relations),
+//                `model/minimax h3/H3Common.swift:389-394` (LSB-first codes)
+#include "mxq_device.hpp"
+#include "mxq_internal.hpp"
+
+namespace mxq {
+namespace {
+
+constexpr int kThreads = 256;
+
+inline unsigned grid_for(int64_t items) {
+  return static_cast<unsigned>((items + kThreads - 1) / kThreads);
+}
+
+// One thread per output word: OR in every code whose bits overlap the word.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void pack_kernel(const uint8_t* __restrict__ codes,
+                                                        int64_t rows, int64_t cols,
+                                                        uint32_t* __restrict__ wq) {
+  const int64_t W = cols * BITS / 32;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= rows * W) return;
+  const int64_t n = idx / W, w = idx - n * W;
+  const uint8_t* row = codes + n * cols;
+  const int64_t bit0 = w * 32;
+  const int64_t k0 = bit0 / BITS, k1 = (bit0 + 31) / BITS;
+  uint32_t word = 0;
+  for (int64_t k = k0; k <= k1; ++k) {
+    const uint32_t c = row[k] & ((1u << BITS) - 1u);
+    const int start = static_cast<int>(k * BITS - bit0);
+    word |= start >= 0 ? (c << start) : (c >> -start);
+  }
+  wq[idx] = word;
+}
+
+// One thread per code.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void unpack_kernel(const uint32_t* __restrict__ wq,
+                                                          int64_t rows, int64_t cols,
+                                                          uint8_t* __restrict__ codes) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= rows * cols) return;
+  const int64_t n = idx / cols, k = idx - n * cols;
+  const uint32_t* row = wq + n * (cols * BITS / 32);
+  const int64_t p = k * BITS;
+  const int off = static_cast<int>(p & 31);
+  uint32_t v = row[p >> 5] >> off;
+  if (off + BITS > 32) v |= row[(p >> 5) + 1] << (32 - off);
+  codes[idx] = static_cast<uint8_t>(v & ((1u << BITS) - 1u));
+}
+
+template <typename T>
+__device__ __forceinline__ float load_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_f32<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_f32<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T>
+__device__ __forceinline__ void store_f32(T* p, float v);
+template <>
+__device__ __forceinline__ void store_f32<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void store_f32<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+
+// One thread per (row, group): min/max, scale/bias, codes, packed words. A
+// group of >= 32 codes always fills whole words, so no two threads share a word.
+template <int BITS, typename TW, typename TSB>
+__global__ __launch_bounds__(kThreads) void quantize_kernel(const TW* __restrict__ w,
+                                                            int64_t rows, int64_t cols, int gs,
+                                                            int mode, uint32_t* __restrict__ wq,
+                                                            TSB* __restrict__ scales,
+                                                            TSB* __restrict__ biases) {
+  const int64_t G = cols / gs;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (gid >= rows * G) return;
+  const int64_t n = gid / G, g = gid - n * G;
+  const TW* wg = w + n * cols + g * gs;
+  const float nmax = static_cast<float>((1 << BITS) - 1);
+  const float eps = 1e-7f;
+
+  float mn = load_f32(wg), mx = mn;
+  for (int i = 1; i < gs; ++i) {
+    const float v = load_f32(wg + i);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  float s, b;
+  if (mode == 0) {
+    s = (mx - mn) / nmax;
+    if (mx == mn) s = eps;
+    b = mn;
+  } else {
+    s = fmaxf((mx - mn) / nmax, eps);
+    const bool side = fabsf(mn) > fabsf(mx);
+    s = side ? s : -s;
+    const float edge = side ? mn : mx;
+    const float q0 = rintf(edge / s);
+    if (q0 != 0.0f) {
+      s = edge / q0;
+      b = edge;
+    } else {
+      b = 0.0f;
+    }
+  }
+
+  uint32_t* out = wq + n * (cols * BITS / 32) + g * (gs * BITS / 32);
+  uint64_t acc = 0;
+  int nacc = 0, wo = 0;
+  for (int i = 0; i < gs; ++i) {
+    float q = rintf((load_f32(wg + i) - b) / s);
+    q = fminf(fmaxf(q, 0.0f), nmax);
+    acc |= static_cast<uint64_t>(static_cast<uint32_t>(q)) << nacc;
+    nacc += BITS;
+    if (nacc >= 32) {
+      out[wo++] = static_cast<uint32_t>(acc);
+      acc >>= 32;
+      nacc -= 32;
+    }
+  }
+  store_f32(scales + gid, s);
+  store_f32(biases + gid, b);
+}
+
+// One thread per period (the smallest run of codes filling whole words).
+template <int BITS, typename TSB, typename TO>
+__global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint32_t* __restrict__ wq,
+                                                              const TSB* __restrict__ scales,
+                                                              const TSB* __restrict__ biases,
+                                                              int64_t rows, int64_t cols, int gs,
+                                                              TO* __restrict__ out) {
+  constexpr int PC = Period<BITS>::codes, PW = Period<BITS>::words;
+  const int64_t per_row = cols / PC;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= rows * per_row) return;
+  const int64_t n = idx / per_row, j = idx - n * per_row;
+  const int64_t k0 = j * PC;
+  const int64_t gi = n * (cols / gs) + k0 / gs;
+  const float s = load_f32(scales + gi), b = load_f32(biases + gi);
+  uint32_t words[PW];
+  const uint32_t* src = wq + n * (cols * BITS / 32) + j * PW;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) words[i] = src[i];
+  uint32_t q[PC];
+  decode_codes<BITS, PC, PW>(words, q);
+  TO* dst = out + n * cols + k0;
+#pragma unroll
+  for (int i = 0; i < PC; ++i) store_f32(dst + i, fmaf(static_cast<float>(q[i]), s, b));
+}
+
+template <template <int> class F, typename... A>
+hipError_t by_bits(int bits, A... args) {
+  switch (bits) {
+    case 2: return F<2>::run(args...);
+    case 3: return F<3>::run(args...);
+    case 4: return F<4>::run(args...);
+    case 5: return F<5>::run(args...);
+    case 6: return F<6>::run(args...);
+    case 8: return F<8>::run(args...);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int BITS>
+struct PackRun {
+  static hipError_t run(const uint8_t* codes, int64_t rows, int64_t cols, uint32_t* wq,
+                        hipStream_t s) {
+    const int64_t items = rows * (cols * BITS / 32);
+    if (items == 0) return hipSuccess;
+    pack_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(codes, rows, cols, wq);
+    return hipGetLastError();
+  }
+};
+
+template <int BITS>
+struct UnpackRun {
+  static hipError_t run(const uint32_t* wq, int64_t rows, int64_t cols, uint8_t* codes,
+                        hipStream_t s) {
+    const int64_t items = rows * cols;
+    if (items == 0) return hipSuccess;
+    unpack_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, rows, cols, codes);
+    return hipGetLastError();
+  }
+};
+
+template <int BITS>
+struct QuantizeRun {
+  template <typename TW, typename TSB>
+  static hipError_t go(const void* w, int64_t rows, int64_t cols, int gs, int mode,
+                       uint32_t* wq, void* sc, void* bi, hipStream_t s) {
+    const int64_t items = rows * (cols / gs);
+    if (items == 0) return hipSuccess;
+    quantize_kernel<BITS, TW, TSB><<<grid_for(items), kThreads, 0, s>>>(
+        static_cast<const TW*>(w), rows, cols, gs, mode, wq, static_cast<TSB*>(sc),
+        static_cast<TSB*>(bi));
+    return hipGetLastError();
+  }
+  static hipError_t run(const void* w, int w_dtype, int64_t rows, int64_t cols, int gs,
+                        int mode, uint32_t* wq, void* sc, void* bi, int sb_dtype,
+                        hipStream_t s) {
+    // dtype codes: 0 = fp32, 1 = bf16
+    if (w_dtype == 0 && sb_dtype == 0)
+      return go<float, float>(w, rows, cols, gs, mode, wq, sc, bi, s);
+    if (w_dtype == 0 && sb_dtype == 1)
+      return go<float, uint16_t>(w, rows, cols, gs, mode, wq, sc, bi, s);
+    if (w_dtype == 1 && sb_dtype == 0)
+      return go<uint16_t, float>(w, rows, cols, gs, mode, wq, sc, bi, s);
+    return go<uint16_t, uint16_t>(w, rows, cols, gs, mode, wq, sc, bi, s);
+  }
+};
+
+template <int BITS>
+struct DequantizeRun {
+  template <typename TSB, typename TO>
+  static hipError_t go(const uint32_t* wq, const void* sc, const void* bi, int64_t rows,
+                       int64_t cols, int gs, void* out, hipStream_t s) {
+    const int64_t items = rows * (cols / Period<BITS>::codes);
+    if (items == 0) return hipSuccess;
+    dequantize_kernel<BITS, TSB, TO><<<grid_for(items), kThreads, 0, s>>>(
+        wq, static_cast<const TSB*>(sc), static_cast<const TSB*>(bi), rows, cols, gs,
+        static_cast<TO*>(out));
+    return hipGetLastError();
+  }
+  static hipError_t run(const uint32_t* wq, const void* sc, const void* bi, int sb_dtype,
+                        int64_t rows, int64_t cols, int gs, void* out, int out_dtype,
+                        hipStream_t s) {
+    if (sb_dtype == 0 && out_dtype == 0)
+      return go<float, float>(wq, sc, bi, rows, cols, gs, out, s);
+    if (sb_dtype == 0 && out_dtype == 1)
+      return go<float, uint16_t>(wq, sc, bi, rows, cols, gs, out, s);
+    if (sb_dtype == 1 && out_dtype == 0)
+      return go<uint16_t, float>(wq, sc, bi, rows, cols, gs, out, s);
+    return go<uint16_t, uint16_t>(wq, sc, bi, rows, cols, gs, out, s);
+  }
+};
+
+}  // namespace
+
+namespace detail {
+
+hipError_t launch_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
+                       hipStream_t s) {
+  return by_bits<PackRun>(bits, codes, rows, cols, wq, s);
+}
+
+hipError_t launch_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits,
+                         uint8_t* codes, hipStream_t s) {
+  return by_bits<UnpackRun>(bits, wq, rows, cols, codes, s);
+}
+
+hipError_t launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int gs,
+                           int bits, int mode, uint32_t* wq, void* scales, void* biases,
+                           int sb_dtype, hipStream_t s) {
+  return by_bits<QuantizeRun>(bits, w, w_dtype, rows, cols, gs, mode, wq, scales, biases,
+                              sb_dtype, s);
+}
+
+hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,
+                             int sb_dtype, int64_t rows, int64_t cols, int gs, int bits,
+                             void* out, int out_dtype, hipStream_t s) {
+  return by_bits<DequantizeRun>(bits, wq, scales, biases, sb_dtype, rows, cols, gs, out,
+                                out_dtype, s);
+}
+
+}  // namespace detail
+}  // namespace mxq

@@ -1,0 +1,246 @@
+// mxq_qmv.hip — small-M quantized matmul (GEMV), y = x * W^T (+ bias).
+//
+// Replaces mlx's qmv path behind quantizedMM for M <= 8: the H3 adaLN /
+// timestep-modulation projection (M = number of unique timesteps,
+// `model/minimax h3/H3Transformer.swift:389-402, 957-988`) and the Gemma-4
+// tied-embedding logits (M = 1, N = 262144,
+// `model/3模块/ltx2.5专属/gemma4文本-(ltx专属).swift:306-312`).
+//
+// HBM-bound: every packed weight byte is read exactly once, with coalesced
+// loads (consecutive lanes read consecutive 16-code chunks of a row). No MFMA.
+// Split-K: the K dimension of each row is spread over the 64 lanes of a wave
+// (and, when N is small, over the 4 waves of a block); partial sums meet in
+// wavefront shuffles and, across waves, in LDS.
+//
+// Per 16-code chunk the affine form is factored:
+//   sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k
+// so each weight costs one decode and MT fused multiply-adds.
+#include "mxq_device.hpp"
+#include "mxq_internal.hpp"
+
+namespace mxq {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+// Codes per chunk: 16, or 32 for the widths whose 16 codes do not fill whole
+// words (3 and 5 bits). A chunk never straddles a group (group size >= 32).
+template <int BITS>
+struct Chunk {
+  static constexpr int codes = (BITS == 3 || BITS == 5) ? 32 : 16;
+  static constexpr int words = codes * BITS / 32;
+};
+
+template <int NW>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[NW]) {
+  if constexpr (NW == 1) {
+    w[0] = p[0];
+  } else if constexpr (NW == 2) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else if constexpr (NW == 3) {
+    const u32x3 v = *reinterpret_cast<const u32x3*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z;
+  } else if constexpr (NW == 4) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+#pragma unroll
+    for (int i = 4; i < NW; ++i) w[i] = p[i];
+  }
+}
+
+// MT: rows of x handled per launch row-block (1, 2, 4 or 8); R: weight rows per
+// wave; KSPLIT: waves of a block sharing the same R rows (1 or 4).
+template <int BITS, int MT, int R, int KSPLIT>
+__global__ __launch_bounds__(kThreads) void qmv_kernel(
+    const uint16_t* __restrict__ x, int M, int K, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases, int N, int gs,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+  constexpr int CC = Chunk<BITS>::codes, CW = Chunk<BITS>::words;
+  constexpr int HALVES = CC / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rows_per_block = R * (kWaves / KSPLIT);
+  const int n0 = blockIdx.x * rows_per_block + (KSPLIT == 1 ? wave : 0) * R;
+  const int m0 = blockIdx.y * MT;
+  const int mcount = min(MT, M - m0);
+  const int64_t W = static_cast<int64_t>(K) * BITS / 32;
+  const int G = K / gs;
+  const int nchunks = K / CC;
+
+  const uint32_t* wrow[R];
+  const uint16_t* srow[R];
+  const uint16_t* brow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(n0 + r, N - 1);
+    wrow[r] = wq + n * W;
+    srow[r] = scales + static_cast<int64_t>(n) * G;
+    brow[r] = biases + static_cast<int64_t>(n) * G;
+  }
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) xrow[m] = x + static_cast<int64_t>(m0 + min(m, mcount - 1)) * K;
+
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+  const int cstep = 64 * KSPLIT;
+  for (int c = lane + 64 * (KSPLIT == 1 ? 0 : wave); c < nchunks; c += cstep) {
+    const int k0 = c * CC;
+    uint32_t words[R][CW];
+    float sc[R], bi[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      load_words<CW>(wrow[r] + static_cast<int64_t>(c) * CW, words[r]);
+      sc[r] = bf16_to_f32(srow[r][k0 / gs]);
+      bi[r] = bf16_to_f32(brow[r][k0 / gs]);
+    }
+    float dot[R][MT], xs[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      xs[m] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) dot[r][m] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      // 16 activations per row of x, as 8 dwords of bf16 pairs
+      uint32_t xv[MT][8];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(xrow[m] + k0 + 16 * h);
+        const u32x4 a = p[0], b = p[1];
+        xv[m][0] = a.x; xv[m][1] = a.y; xv[m][2] = a.z; xv[m][3] = a.w;
+        xv[m][4] = b.x; xv[m][5] = b.y; xv[m][6] = b.z; xv[m][7] = b.w;
+      }
+      float xf[MT][16];
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xf[m][2 * i] = __uint_as_float(xv[m][i] << 16);
+          xf[m][2 * i + 1] = __uint_as_float(xv[m][i] & 0xFFFF0000u);
+          xs[m] += xf[m][2 * i] + xf[m][2 * i + 1];
+        }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        uint32_t q[CC];
+        decode_codes<BITS, CC, CW>(words[r], q);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float qf = static_cast<float>(q[16 * h + i]);
+#pragma unroll
+          for (int m = 0; m < MT; ++m) dot[r][m] = fmaf(xf[m][i], qf, dot[r][m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r][m] = fmaf(sc[r], dot[r][m], fmaf(bi[r], xs[m], acc[r][m]));
+  }
+
+  // wave reduction: afterwards every lane holds every total
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum(acc[r][m]);
+
+  if constexpr (KSPLIT > 1) {
+    __shared__ float part[KSPLIT][R * MT];
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) part[wave][r * MT + m] = acc[r][m];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KSPLIT; ++w) t += part[w][r * MT + m];
+        acc[r][m] = t;
+      }
+  }
+
+  // lane j writes output j = r*MT + m
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (lane == r * MT + m) {
+        const int n = n0 + r;
+        if (n < N && m < mcount) {
+          float v = acc[r][m];
+          if (bias) v += bf16_to_f32(bias[n]);
+          y[static_cast<int64_t>(m0 + m) * N + n] = f32_to_bf16(v);
+        }
+      }
+    }
+}
+
+template <int BITS, int MT, int R, int KSPLIT>
+hipError_t run_qmv(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                   const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                   hipStream_t s) {
+  const int rows_per_block = R * (kWaves / KSPLIT);
+  dim3 grid((N + rows_per_block - 1) / rows_per_block, (M + MT - 1) / MT);
+  qmv_kernel<BITS, MT, R, KSPLIT><<<grid, kThreads, 0, s>>>(x, M, K, wq, sc, bi, N, gs, bias, y);
+  return hipGetLastError();
+}
+
+template <int BITS, int MT>
+hipError_t pick_split(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                      const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                      hipStream_t s) {
+  constexpr int R = MT >= 4 ? 4 : 8;
+  // Enough waves to cover every CU several times over without splitting K
+  // across waves; otherwise split each row's K range over the 4 waves.
+  const int64_t waves = (static_cast<int64_t>(N) + R - 1) / R;
+  if (waves >= 2048) return run_qmv<BITS, MT, R, 1>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  return run_qmv<BITS, MT, R, 4>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+}
+
+template <int BITS>
+hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                   const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                   hipStream_t s) {
+  if (M <= 1) return pick_split<BITS, 1>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (M <= 2) return pick_split<BITS, 2>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (M <= 4) return pick_split<BITS, 4>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  return pick_split<BITS, 8>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+}
+
+}  // namespace
+
+namespace detail {
+
+hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,
+                      const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
+                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  switch (bits) {
+    case 2: return pick_mt<2>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 3: return pick_mt<3>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 4: return pick_mt<4>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 5: return pick_mt<5>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 6: return pick_mt<6>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 8: return pick_mt<8>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace detail
+}  // namespace mxq

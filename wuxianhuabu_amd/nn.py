@@ -1,0 +1,144 @@
+"""Module types of the quantized-linear path: QuantizedLinear and MfLinear.
+
+QuantizedLinear mirrors MLXNN's QuantizedLinear as the reference uses it:
+    QuantizedLinear(inDims, outDims, bias:, groupSize:, bits:)
+        `model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:177-188, 387-388`
+    parameters weight (uint32 packed), scales, biases, optional bias, loaded by
+    update(parameters:) from keys X.weight / X.scales / X.biases
+        `model/4 组装实现&调用/ltx2.5-(ltx专属).swift:576-581`
+    callAsFunction(x) = quantizedMatmul(x, weight, scales, biases, transpose: true,
+        groupSize, bits) + bias
+
+MfLinear mirrors the reference's own wrapper (`model/minimax h3/H3Common.swift:283-377`):
+load() infers bits = 32*wCols/in and groupSize = in/sCols, casts scales/biases
+to the compute dtype; forward() casts x to bf16, runs the quantized matmul,
+then adds the bias. Here the bias add is fused into the kernel epilogue (added
+in fp32 before the single bf16 rounding).
+"""
+import math
+
+import torch
+
+from . import ops
+from .weights import get_quantized, infer_geometry
+
+
+class QuantizedLinear:
+    def __init__(self, input_dims, output_dims, bias=True, group_size=64, bits=4,
+                 device="cuda", seed=None):
+        # MLXNN initialises uniform(-1/sqrt(in), 1/sqrt(in)) and quantizes it.
+        self.input_dims = int(input_dims)
+        self.output_dims = int(output_dims)
+        self.group_size = int(group_size)
+        self.bits = int(bits)
+        g = torch.Generator(device="cpu")
+        if seed is not None:
+            g.manual_seed(seed)
+        scale = math.sqrt(1.0 / self.input_dims)
+        w = (torch.rand(self.output_dims, self.input_dims, generator=g) * 2 - 1) * scale
+        w = w.to(device=device, dtype=torch.bfloat16)
+        self.weight, self.scales, self.biases = ops.quantized(w, self.group_size, self.bits)
+        self.bias = (torch.zeros(self.output_dims, dtype=torch.bfloat16, device=device)
+                     if bias else None)
+
+    @classmethod
+    def from_weights(cls, weight, scales, biases, bias=None, group_size=64, bits=4):
+        """Wrap an existing packed triple (as update(parameters:) does)."""
+        obj = cls.__new__(cls)
+        obj.weight = weight
+        obj.scales = scales
+        obj.biases = biases
+        obj.bias = bias
+        obj.group_size = int(group_size)
+        obj.bits = int(bits)
+        obj.output_dims = int(weight.shape[0])
+        obj.input_dims = int(weight.shape[1] * 32 // bits)
+        return obj
+
+    @classmethod
+    def from_linear(cls, weight, bias=None, group_size=64, bits=4, mode="minmax"):
+        """Quantize a dense [out, in] weight (MLXNN QuantizedLinear.from(linear:))."""
+        wq, s, b = ops.quantized(weight.contiguous(), group_size, bits, mode=mode)
+        return cls.from_weights(wq, s, b, bias, group_size, bits)
+
+    def update(self, parameters):
+        """Load weight/scales/biases/bias from a mapping of tensors."""
+        for key in ("weight", "scales", "biases"):
+            if key not in parameters:
+                raise KeyError(f"QuantizedLinear.update: missing '{key}'")
+        self.weight = parameters["weight"]
+        self.scales = parameters["scales"]
+        self.biases = parameters["biases"]
+        if "bias" in parameters:
+            self.bias = parameters["bias"]
+        self.output_dims = int(self.weight.shape[0])
+        self.input_dims = int(self.weight.shape[1] * 32 // self.bits)
+        return self
+
+    @property
+    def shape(self):
+        return (self.output_dims, self.input_dims)
+
+    def __call__(self, x):
+        return ops.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
+                                    group_size=self.group_size, bits=self.bits, bias=self.bias)
+
+    callAsFunction = __call__
+
+
+class MfLinear:
+    """Dense-or-affine-quantized linear, loaded from a weights mapping."""
+
+    def __init__(self, in_dim, out_dim=0):
+        self.in_dim = int(in_dim)
+        self.out_dim = int(out_dim)
+        self.is_quantized = False
+        self.w = None
+        self.scales = None
+        self.biases = None
+        self.bias = None
+        self.bits = 0
+        self.group_size = 0
+
+    @classmethod
+    def load(cls, weights, prefix, in_features, dtype=torch.bfloat16):
+        """`H3Common.swift:312-338`: quantized triple if present, else dense [out, in]."""
+        lin = cls(in_features)
+        q = get_quantized(weights, prefix)
+        if q is not None:
+            w, s, b = q
+            if w.ndim != 2:
+                raise ValueError(f"bad file: quantized weight rank {w.ndim}")
+            lin.out_dim = int(w.shape[0])
+            lin.is_quantized = True
+            lin.w = w
+            lin.bits, lin.group_size = infer_geometry(int(w.shape[1]), int(s.shape[1]),
+                                                      in_features)
+            lin.scales = s.to(dtype).contiguous()
+            lin.biases = b.to(dtype).contiguous()
+        else:
+            raw = weights.get(prefix + ".weight")
+            if raw is None:
+                raise KeyError(f"missing weight: {prefix}.weight")
+            lin.out_dim = int(raw.shape[0])
+            lin.w = raw.t().to(dtype).contiguous()  # dense, pre-transposed [in, out]
+        b = weights.get(prefix + ".bias")
+        if b is not None:
+            lin.bias = b.to(dtype).contiguous()
+        return lin
+
+    def forward(self, x):
+        if self.is_quantized:
+            if self.scales.dtype != torch.bfloat16:
+                raise ValueError("MfLinear: the quantized kernels take bfloat16 scales/biases")
+            xc = x.to(torch.bfloat16).contiguous()
+            return ops.quantized_matmul(xc, self.w, self.scales, self.biases, transpose=True,
+                                        group_size=self.group_size, bits=self.bits,
+                                        bias=self.bias)
+        # dense branch: not part of the quantized path; plain device matmul
+        out = x.to(self.w.dtype) @ self.w
+        if self.bias is not None:
+            out = out + self.bias
+        return out
+
+    __call__ = forward

@@ -1,0 +1,219 @@
+"""The MLX-Swift quantization operators, over torch device tensors.
+
+Same names, argument meaning and error behaviour as the functions the
+reference calls through MLX-Swift:
+
+    quantized(w, group_size=64, bits=4)            mlx `quantized(_:groupSize:bits:)`
+        `model/minimax h3/tools/quantize_h3_g64.py:132` (mx.quantize),
+        `Packages/z-image-swift/Sources/ZImage/Weights.swift:31`
+    dequantized(w, scales, biases, group_size, bits)
+        `model/minimax h3/H3Common.swift:382-401` (MfLinear.dequantizedWeight)
+    quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+        `model/minimax h3/H3Common.swift:358-359` (quantizedMM),
+        `model/3模块/ltx2.5专属/gemma4文本-(ltx专属).swift:306-312` (quantizedMatmul)
+
+torch supplies device memory and the current HIP stream; all arithmetic runs in
+libmxq.so (HIP, gfx950). Invalid arguments raise ValueError with mlx's wording.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+_SB_DTYPES = {torch.float32: _lib.MXQ_FLOAT32, torch.bfloat16: _lib.MXQ_BFLOAT16}
+_SUPPORTED_BITS = (2, 3, 4, 5, 6, 8)
+_SUPPORTED_GS = (32, 64, 128)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _on_gpu(op, *tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"[{op}] all arrays must be on the GPU (got {t.device}).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"[{op}] all arrays must be on the same device.")
+
+
+def _dense(t):
+    """Row-major copy of a strided view (mlx accepts any strides; the kernels
+    read contiguous rows)."""
+    return t if t is None or t.is_contiguous() else t.contiguous()
+
+
+def _check_bits_gs(op, bits, group_size):
+    if bits not in _SUPPORTED_BITS:
+        raise ValueError(f"[{op}] The requested number of bits {bits} is not supported. "
+                         "The supported bits are 2, 3, 4, 5, 6 and 8.")
+    if group_size not in _SUPPORTED_GS:
+        raise ValueError(f"[{op}] The requested group size {group_size} is not supported. "
+                         "The supported group sizes are 32, 64, and 128.")
+
+
+def _as_words(w):
+    if w.dtype == torch.uint32:
+        return w
+    if w.dtype == torch.int32:
+        return w.view(torch.uint32)
+    raise ValueError(f"packed weights must be uint32 (got {w.dtype}).")
+
+
+def quantized(w, group_size=64, bits=4, *, mode="minmax"):
+    """Quantize w [..., K] along its last axis -> (wq uint32, scales, biases).
+
+    scales/biases have w's dtype (float32 or bfloat16) and shape [..., K/group_size];
+    wq has shape [..., K*bits/32]. mode "minmax": scale=(max-min)/(2^bits-1),
+    bias=min; mode "mlx_edge": mlx's sign-aware edge quantizer.
+    """
+    _check_bits_gs("quantize", bits, group_size)
+    if w.ndim < 2:
+        raise ValueError(f"[quantize] The matrix to be quantized must have at least 2 "
+                         f"dimensions but it has only {w.ndim}.")
+    K = w.shape[-1]
+    if K % group_size != 0:
+        raise ValueError(f"[quantize] The last dimension of the matrix needs to be divisible "
+                         f"by the quantization group size {group_size}. However the provided "
+                         f"matrix has shape {tuple(w.shape)}")
+    if w.dtype not in _SB_DTYPES:
+        raise ValueError(f"[quantize] Only float32 and bfloat16 weights are supported "
+                         f"(got {w.dtype}).")
+    modes = {"minmax": _lib.MXQ_MODE_MINMAX, "mlx_edge": _lib.MXQ_MODE_MLX_EDGE}
+    if mode not in modes:
+        raise ValueError(f"[quantize] unknown mode {mode!r}")
+    _on_gpu("quantize", w)
+    w = _dense(w)
+    lead = tuple(w.shape[:-1])
+    rows = w.numel() // K if K else 0
+    wq = torch.empty(lead + (K * bits // 32,), dtype=torch.uint32, device=w.device)
+    scales = torch.empty(lead + (K // group_size,), dtype=w.dtype, device=w.device)
+    biases = torch.empty_like(scales)
+    dt = _SB_DTYPES[w.dtype]
+    _lib.check(_lib.lib().mxq_quantize(_ptr(w), dt, rows, K, group_size, bits, modes[mode],
+                                       _ptr(wq), _ptr(scales), _ptr(biases), dt, _stream(w)))
+    return wq, scales, biases
+
+
+def dequantized(w, scales, biases, group_size=64, bits=4, *, dtype=None):
+    """w = q*scale + bias -> [..., K] in scales' dtype (or `dtype`)."""
+    _check_bits_gs("dequantize", bits, group_size)
+    w = _as_words(w)
+    _on_gpu("dequantize", w, scales, biases)
+    w, scales, biases = _dense(w), _dense(scales), _dense(biases)
+    K = w.shape[-1] * 32 // bits
+    if w.shape[-1] * 32 % bits != 0:
+        raise ValueError("[dequantize] The packed width is not a whole number of codes.")
+    if scales.shape != biases.shape or tuple(scales.shape[:-1]) != tuple(w.shape[:-1]) or \
+            scales.shape[-1] * group_size != K:
+        raise ValueError(f"[dequantize] Shape of scales and biases does not match the matrix "
+                         f"given the quantization parameters. Provided matrix of shape "
+                         f"{tuple(w.shape)} and scales/biases of shape {tuple(scales.shape)} "
+                         f"with group_size={group_size} and bits={bits}.")
+    if scales.dtype not in _SB_DTYPES or biases.dtype != scales.dtype:
+        raise ValueError("[dequantize] scales and biases must both be float32 or bfloat16.")
+    out_dtype = scales.dtype if dtype is None else dtype
+    if out_dtype not in _SB_DTYPES:
+        raise ValueError("[dequantize] output dtype must be float32 or bfloat16.")
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    out = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=out_dtype, device=w.device)
+    _lib.check(_lib.lib().mxq_dequantize(_ptr(w), _ptr(scales), _ptr(biases),
+                                         _SB_DTYPES[scales.dtype], rows, K, group_size, bits,
+                                         _ptr(out), _SB_DTYPES[out_dtype], _stream(w)))
+    return out
+
+
+def _matmul_shapes(op, x, w, scales, biases, group_size, bits, bias):
+    _check_bits_gs(op, bits, group_size)
+    w = _as_words(w)
+    _on_gpu(op, x, w, scales, biases, bias)
+    if w.ndim != 2:
+        raise ValueError(f"[{op}] The weight matrix must be 2-D (got {w.ndim}-D).")
+    N = w.shape[0]
+    K = x.shape[-1]
+    if w.shape[1] * 32 != K * bits:
+        raise ValueError(f"[{op}] The shapes of the weight and scales are incompatible "
+                         f"based on bits and group_size. w.shape() == {tuple(w.shape)} and "
+                         f"x.shape() == {tuple(x.shape)} with bits={bits}")
+    if tuple(scales.shape) != (N, K // group_size) or scales.shape != biases.shape or \
+            K % group_size != 0:
+        raise ValueError(f"[{op}] The shapes of the weight and scales are incompatible "
+                         f"based on bits and group_size. w.shape() == {tuple(w.shape)} and "
+                         f"scales.shape() == {tuple(scales.shape)} with group_size="
+                         f"{group_size} and bits={bits}")
+    if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or \
+            biases.dtype != torch.bfloat16:
+        raise ValueError(f"[{op}] x, scales and biases must be bfloat16 "
+                         f"(got {x.dtype}, {scales.dtype}, {biases.dtype}).")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (N,)):
+        raise ValueError(f"[{op}] bias must be bfloat16 of shape ({N},).")
+    return _dense(x), _dense(w), _dense(scales), _dense(biases), _dense(bias), N, K
+
+
+def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4, *,
+                     bias=None, path="auto"):
+    """y [..., N] = x [..., K] @ dequantized(w)^T (+ bias), bf16 in/out, fp32 accumulate.
+
+    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv" to force a kernel.
+    """
+    op = "quantized_matmul"
+    x, w, scales, biases, bias, N, K = _matmul_shapes(op, x, w, scales, biases, group_size,
+                                                      bits, bias)
+    lead = tuple(x.shape[:-1])
+    M = x.numel() // K if K else 0
+    y = torch.empty(lead + (N,), dtype=torch.bfloat16, device=x.device)
+    L = _lib.lib()
+    args = (_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N)
+    if path == "auto":
+        rc = L.mxq_quantized_matmul(*args, 1 if transpose else 0, group_size, bits, _ptr(bias),
+                                    _ptr(y), _stream(x))
+    elif not transpose:
+        raise NotImplementedError("[quantized_matmul] transpose=False is not implemented.")
+    elif path == "qmm":
+        rc = L.mxq_qmm(*args, group_size, bits, _ptr(bias), _ptr(y), _stream(x))
+    elif path == "qmv":
+        rc = L.mxq_qmv(*args, group_size, bits, _ptr(bias), _ptr(y), _stream(x))
+    else:
+        raise ValueError(f"unknown path {path!r}")
+    _lib.check(rc)
+    return y
+
+
+# camelCase aliases, as the Swift surface spells them
+quantizedMatmul = quantized_matmul
+quantizedMM = quantized_matmul
+
+
+def pack(codes, bits):
+    """codes uint8 [..., K] -> wq uint32 [..., K*bits/32] (MLX bitstream)."""
+    if codes.dtype != torch.uint8:
+        raise ValueError("[pack] codes must be uint8.")
+    _on_gpu("pack", codes)
+    codes = _dense(codes)
+    K = codes.shape[-1]
+    rows = codes.numel() // K if K else 0
+    wq = torch.empty(tuple(codes.shape[:-1]) + (K * bits // 32,), dtype=torch.uint32,
+                     device=codes.device)
+    _lib.check(_lib.lib().mxq_pack(_ptr(codes), rows, K, bits, _ptr(wq), _stream(codes)))
+    return wq
+
+
+def unpack(w, bits):
+    """wq uint32 [..., W] -> codes uint8 [..., W*32/bits]."""
+    w = _dense(_as_words(w))
+    _on_gpu("unpack", w)
+    K = w.shape[-1] * 32 // bits
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    codes = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=torch.uint8, device=w.device)
+    _lib.check(_lib.lib().mxq_unpack(_ptr(w), rows, K, bits, _ptr(codes), _stream(w)))
+    return codes
