@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Benchmark of the MLX affine quantized linear on one MI355X.
+
+Headline (one "step" = one quantized-matmul launch over the whole batch):
+  qmm : 6-bit gs64 QuantizedLinear, x bf16 [14400, 4096] ~ N(0,1), W [16384, 4096]
+        from N(0, 0.02) (min/max quantizer, bf16 scales/biases) -> y bf16 [14400, 16384]
+        (the 720p DiT MLP up projection). value = 2*M*N*K / t in TFLOP/s.
+  gemv: 6-bit gs64, x [2, 4096], W [24576, 4096] -> y [2, 24576] (adaLN modulation for
+        a CFG pair), reported in GB/s of algorithmic bytes; 5 weight copies (410 MB,
+        above the 256 MB Infinity Cache) are rotated so every launch reads HBM.
+Inputs are seeded synthetic tensors generated on the GPU and resident in HBM before
+timing starts. The CPU baseline (the oracle's restatement of mlx's CPU quantized
+matmul loop, timed on this host) and a sampled-row correctness check run after the
+GPU timing; they are the only part of this file that touches the oracle.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--all]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
+
+QMM = dict(name="qmm 6-bit gs64 M=14400 K=4096 N=16384 (720p DiT MLP up projection)",
+           M=14400, K=4096, N=16384, gs=64, bits=6, seed=3)
+GEMV = dict(name="gemv 6-bit gs64 M=2 K=4096 N=24576 (adaLN modulation, CFG pair)",
+            M=2, K=4096, N=24576, gs=64, bits=6, seed=2, copies=5)
+EXTRA = [
+    dict(name="c0 6-bit M=256 K=2048 N=2048", M=256, K=2048, N=2048, gs=64, bits=6, seed=0),
+    dict(name="c1 6-bit M=3600 K=4096 N=4096", M=3600, K=4096, N=4096, gs=64, bits=6, seed=1),
+    dict(name="c3 down 6-bit M=14400 K=16384 N=4096 (GELU input)", M=14400, K=16384, N=4096,
+         gs=64, bits=6, seed=13, gelu=True),
+]
+C4_CHAIN = [  # 4-bit gs64 DiT block linear chain, weights resident
+    ("qkv", 14400, 4096, 12288), ("out", 14400, 4096, 4096), ("xq", 14400, 4096, 4096),
+    ("xkv", 512, 4096, 8192), ("up", 14400, 4096, 16384), ("down", 14400, 16384, 4096),
+]
+
+
+def weight_bytes(N, K, bits, gs):
+    return N * K * bits // 8 + 2 * (N * (K // gs)) * 2
+
+
+def gemv_bytes(c):
+    M, N, K = c["M"], c["N"], c["K"]
+    return weight_bytes(N, K, c["bits"], c["gs"]) + M * K * 2 + M * N * 2
+
+
+def make_inputs(torch, mx, c, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(1000 + c["seed"])
+    x = torch.randn(c["M"], c["K"], generator=g, device=dev)
+    if c.get("gelu"):
+        x = torch.nn.functional.gelu(x.bfloat16().float(), approximate="tanh")
+    x = x.bfloat16()
+    g.manual_seed(2000 + c["seed"])
+    w = torch.randn(c["N"], c["K"], generator=g, device=dev) * 0.02
+    wq, s, b = mx.quantized(w, c["gs"], c["bits"], scales_dtype=torch.bfloat16)
+    del w
+    return x, wq, s, b
+
+
+def time_launches(torch, fn, steps, warmup, rotate=1):
+    """Per-launch durations (ms) from HIP events on the launching stream."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        fn(i % rotate)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    total = ev[0].elapsed_time(ev[steps])
+    return per, total
+
+
+def load_traffic(kernel_key):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    scaled by a copy-kernel calibration; committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
+    """The oracle, as checker and as the CPU baseline (this host's cores)."""
+    import numpy as np
+    from oracle import pyoracle as O
+    import torch
+
+    def host_u16(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def host_u32(t):
+        return t.contiguous().view(torch.int32).cpu().numpy().view(np.uint32)
+
+    out = {}
+    # -- correctness on sampled rows (qmm) and on the full GEMV output --
+    x, wq, s, b, y = bufs["qmm"]
+    rng = np.random.default_rng(7)
+    rows = np.unique(np.concatenate([rng.choice(qmm_c["M"], 24, replace=False),
+                                     [qmm_c["M"] - 1]]))
+    xh = host_u16(x)
+    wqh, sh, bh = host_u32(wq), host_u16(s), host_u16(b)
+    yg = y.float()[torch.as_tensor(rows, device=y.device)].cpu().numpy().astype(np.float64)
+    threads = min(16, os.cpu_count() or 1)
+    ref_w = O.qmm_f64_bf16w(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], rows=rows,
+                            threads=threads)
+    ref = O.qmm_f64(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], rows=rows, threads=threads)
+    out["qmm_check"] = {
+        "rows": int(len(rows)),
+        "max_rel_vs_exact": float(np.abs(yg - ref).max() / np.abs(ref).max()),
+        "max_rel_vs_bf16w": float(np.abs(yg - ref_w).max() / np.abs(ref_w).max()),
+        "cosine": float((yg.ravel() @ ref.ravel()) /
+                        (np.linalg.norm(yg) * np.linalg.norm(ref))),
+    }
+    gx, gwq, gs_, gb, gy = bufs["gemv"]
+    gref = O.qmm_f64(host_u16(gx), host_u32(gwq), host_u16(gs_), host_u16(gb), gemv_c["gs"],
+                     gemv_c["bits"], threads=threads)
+    gyh = gy.float().cpu().numpy().astype(np.float64)
+    out["gemv_check"] = {"max_rel_vs_exact": float(np.abs(gyh - gref).max() / np.abs(gref).max())}
+
+    # -- CPU baseline: mlx CPU qmm loop structure, bf16 arithmetic, 1 core --
+    K, N = qmm_c["K"], qmm_c["N"]
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=1)
+    t_row = time.perf_counter() - t0
+    nrows = int(max(1, min(64, budget_s / max(t_row, 1e-3))))
+    sample = np.arange(nrows, dtype=np.int64)
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=sample, threads=1)
+    t = time.perf_counter() - t0
+    flops = 2.0 * nrows * N * K
+    out["cpu_baseline"] = {
+        "value": flops / t / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+        "sample": f"{nrows} of {qmm_c['M']} rows of the qmm workload (mlx CPU qmm loop "
+                  f"restated in C, bf16 arithmetic), {t:.1f} s; the loop is linear in M",
+    }
+    # GEMV on the CPU: the full M=2 workload, 1 core
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(host_u16(gx), host_u32(gwq), host_u16(gs_), host_u16(gb), gemv_c["gs"],
+                  gemv_c["bits"], accum=0, threads=1)
+    tg = time.perf_counter() - t0
+    out["cpu_baseline_gemv"] = {"value": gemv_bytes(gemv_c) / tg / 1e9, "unit": "GB/s",
+                                "cores": 1, "kind": "port",
+                                "sample": f"full M=2 workload, {tg:.2f} s"}
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")),
+                         "unknown")
+    except OSError:
+        model = "unknown"
+    out["cpu_host"] = {"model": model, "nproc": os.cpu_count()}
+    results.update(out)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip oracle check and CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    ap.add_argument("--all", action="store_true", help="also time c0, c1, c3-down, c4 chain")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the quantized linear is benchmarked on a single "
+              "MI355X (multi-GPU sharding is a design note, not part of this build).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import wuxianhuabu_amd as mx
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    steps, warmup = args.steps, args.warmup
+    res = {}
+
+    # ---------------- qmm (headline) ----------------
+    c = QMM
+    x, wq, s, b = make_inputs(torch, mx, c, dev)
+    y = torch.empty(c["M"], c["N"], dtype=torch.bfloat16, device=dev)
+    L = mx.lib()
+    import ctypes
+
+    def qmm_launch(_i, x=x, wq=wq, s=s, b=b, y=y, c=c):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.mxq_qmm(ctypes.c_void_p(x.data_ptr()), c["M"], c["K"],
+                       ctypes.c_void_p(wq.data_ptr()), ctypes.c_void_p(s.data_ptr()),
+                       ctypes.c_void_p(b.data_ptr()), c["N"], c["gs"], c["bits"], None,
+                       ctypes.c_void_p(y.data_ptr()), st)
+        if rc:
+            raise RuntimeError(L.mxq_last_error().decode())
+
+    torch.cuda.synchronize()
+    per, total = time_launches(torch, qmm_launch, steps, warmup)
+    flop = 2.0 * c["M"] * c["N"] * c["K"]
+    per_sorted = sorted(per)
+    avg_ms = sum(per) / len(per)
+    med_ms = per_sorted[len(per) // 2]
+    qmm_tflops = flop / (total / steps * 1e-3) / 1e12
+    achieved = flop / (avg_ms * 1e-3) / 1e12
+    print(f"[bench] qmm: avg {avg_ms:.3f} ms  median {med_ms:.3f} ms  "
+          f"{achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    # ---------------- gemv ----------------
+    g = GEMV
+    gx, gwq, gs_, gb = make_inputs(torch, mx, g, dev)
+    copies = [(gwq, gs_, gb)]
+    for _ in range(g["copies"] - 1):
+        copies.append((gwq.clone(), gs_.clone(), gb.clone()))
+    gy = torch.empty(g["M"], g["N"], dtype=torch.bfloat16, device=dev)
+
+    def gemv_launch(i, gx=gx, gy=gy, g=g):
+        wq_i, s_i, b_i = copies[i]
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = L.mxq_qmv(ctypes.c_void_p(gx.data_ptr()), g["M"], g["K"],
+                       ctypes.c_void_p(wq_i.data_ptr()), ctypes.c_void_p(s_i.data_ptr()),
+                       ctypes.c_void_p(b_i.data_ptr()), g["N"], g["gs"], g["bits"], None,
+                       ctypes.c_void_p(gy.data_ptr()), st)
+        if rc:
+            raise RuntimeError(L.mxq_last_error().decode())
+
+    gsteps = max(steps * 10, 100)
+    gper, gtotal = time_launches(torch, gemv_launch, gsteps, warmup * 10, rotate=g["copies"])
+    gbytes = gemv_bytes(g)
+    gavg = sum(gper) / len(gper)
+    gemv_gbs = gbytes / (gavg * 1e-3) / 1e9
+    print(f"[bench] gemv: avg {gavg * 1e3:.2f} us  {gemv_gbs:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    res["gemv"] = {
+        "metric": "GEMV GB/s at M=2", "value": gemv_bytes(g) / (gtotal / gsteps * 1e-3) / 1e9,
+        "unit": "GB/s", "us_per_launch": gavg * 1e3, "launches": gsteps,
+        "config": {"workload": g["name"], "weight_copies_rotated": g["copies"],
+                   "bytes_per_launch": gbytes},
+        "roofline": {"bound": "hbm", "achieved": gemv_gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": gemv_gbs / HBM_PEAK_GBS,
+                     "traffic": load_traffic("qmv_c2")},
+    }
+
+    # ---------------- optional extra configs ----------------
+    if args.all:
+        extra = {}
+        for e in EXTRA:
+            ex, ewq, es, eb = make_inputs(torch, mx, e, dev)
+
+            def f(_i, ex=ex, ewq=ewq, es=es, eb=eb, e=e):
+                mx.quantized_matmul(ex, ewq, es, eb, group_size=e["gs"], bits=e["bits"])
+
+            p, t = time_launches(torch, f, max(5, steps // 2), 2)
+            a = sum(p) / len(p)
+            extra[e["name"]] = {"ms": a, "tflops": 2.0 * e["M"] * e["N"] * e["K"] / a / 1e9}
+            del ex, ewq, es, eb
+        chain = []
+        for i, (nm, M, K, N) in enumerate(C4_CHAIN):
+            cc = dict(M=M, K=K, N=N, gs=64, bits=4, seed=40 + i)
+            chain.append((cc,) + make_inputs(torch, mx, cc, dev))
+
+        def run_chain(_i):
+            for cc, cx, cwq, cs, cb in chain:
+                mx.quantized_matmul(cx, cwq, cs, cb, group_size=64, bits=4)
+
+        p, t = time_launches(torch, run_chain, max(5, steps // 2), 2)
+        a = sum(p) / len(p)
+        fl = sum(2.0 * M * N * K for _, M, K, N in C4_CHAIN)
+        extra["c4 4-bit DiT block chain"] = {"ms": a, "tflops": fl / a / 1e9}
+        res["extra"] = extra
+        del chain
+
+    # ---------------- CPU leg (oracle) ----------------
+    if not args.no_cpu:
+        cpu_leg(res, {"qmm": (x, wq, s, b, y), "gemv": (gx, gwq, gs_, gb, gy)}, QMM, GEMV,
+                args.cpu_budget)
+
+    line = {
+        "metric": "6-bit qmm TFLOP/s (M=14400, 4096->16384) + GEMV GB/s at M=2",
+        "value": qmm_tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": total / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.randn on the GPU; W quantized by libmxq min/max)",
+        "config": {"workload": QMM["name"], "M": QMM["M"], "K": QMM["K"], "N": QMM["N"],
+                   "bits": QMM["bits"], "group_size": QMM["gs"]},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
+                     "traffic": load_traffic("qmm_c3_up"),
+                     "kernel_avg_ms": avg_ms, "kernel_median_ms": med_ms},
+    }
+    line.update(res)
+    if "cpu_baseline" not in line:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

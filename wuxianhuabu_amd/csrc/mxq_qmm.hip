@@ -7,21 +7,23 @@
 // `model/minimax h3/H3Transformer.swift:448, 580, 622, 627`, and MLXNN
 // QuantizedLinear in `model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:177-188, 387-388`).
 //
-// Work decomposition (one workgroup = 4 waves = 256 threads):
+// Work decomposition (one workgroup = 4 waves = 256 threads, one per SIMD):
 //   * the workgroup owns a BM x 256 output tile (BM tokens x 256 features);
 //   * each wave owns BM x 64: it loads the packed codes of its 64 feature rows
-//     straight from HBM (one 16-code chunk per lane per 16-row block), unpacks
+//     with buffer loads (one 32-code run per lane per 32-row block), unpacks
 //     them in registers to bf16 (w = q*s + b in fp32, then round) and keeps
 //     them as MFMA operands for the whole K step;
 //   * the BM x 64 activation tile of each K step is staged once through LDS
 //     (double-buffered) and read by all four waves;
-//   * v_mfma_f32_16x16x32_bf16 with the weights as the A operand and the
-//     activations as the B operand, so each lane's accumulator holds 4
-//     consecutive output features of one token (8-byte stores).
-// K is consumed 64 codes at a time. Inside one 64-wide step, lane group
-// g4 = lane/16 owns codes [16*g4, 16*g4+16) of its row for both the weight and
-// the activation fragments, so each lane unpacks one contiguous 16-code run
-// (BITS/2 whole words) and reads 32 contiguous activation bytes.
+//   * v_mfma_f32_32x32x16_bf16 with the weights as the A operand and the
+//     activations as the B operand; each lane's 16 accumulators hold one token
+//     and four runs of 4 consecutive output features (8-byte stores).
+// K is consumed 64 codes at a time. Inside one 64-wide step, lane half
+// g2 = lane/32 owns codes [32*g2, 32*g2+32) of its row for both the weight and
+// the activation fragments, so each lane unpacks one contiguous 32-code run
+// (BITS whole words, for every supported width) and reads 64 contiguous
+// activation bytes. The loop is software-pipelined: packed weights for step
+// k+2 are loaded and step k+1 is unpacked while step k's MFMAs run.
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
 
@@ -33,55 +35,88 @@ constexpr int kKS = 64;        // K step
 constexpr int kXPitch = 72;    // LDS row pitch in bf16 (64 + 8 padding)
 constexpr int kThreads = 256;
 
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t v3u __attribute__((ext_vector_type(3)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// Raw buffer loads: 64-bit base in the (wave-uniform) descriptor, a per-lane
+// 32-bit byte offset computed once, and the K-step advance as a scalar offset.
 template <int NW>
-__device__ __forceinline__ void load_chunk(const uint32_t* p, uint32_t (&w)[NW]) {
-  if constexpr (NW == 1) {
-    w[0] = p[0];
-  } else if constexpr (NW == 2) {
-    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+__device__ __forceinline__ void buf_load_words(__amdgpu_buffer_rsrc_t r, int voff, int soff,
+                                               uint32_t (&w)[NW]) {
+  if constexpr (NW == 2) {
+    const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
     w[0] = v.x; w[1] = v.y;
   } else if constexpr (NW == 3) {
-    const u32x3 v = *reinterpret_cast<const u32x3*>(p);
+    const v3u v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0);
     w[0] = v.x; w[1] = v.y; w[2] = v.z;
-  } else {
-    static_assert(NW == 4, "unsupported chunk");
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  } else if constexpr (NW == 4) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (NW == 5) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    w[4] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 16, soff, 0);
+  } else if constexpr (NW == 6) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const v2u u = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 16, soff, 0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; w[4] = u.x; w[5] = u.y;
+  } else {
+    static_assert(NW == 8, "unsupported run");
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const v4u u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    w[4] = u.x; w[5] = u.y; w[6] = u.z; w[7] = u.w;
   }
 }
 
-// 16 codes -> two MFMA operands of 8 bf16 each (w = q*s + b, fp32 then RNE).
-template <int BITS, int NW>
-__device__ __forceinline__ void unpack16(const uint32_t (&w)[NW], float s, float b,
-                                         bf16x8& lo, bf16x8& hi) {
-  uint32_t q[16];
-  decode_codes<BITS, 16, NW>(w, q);
-  uint32_t p[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    p[i] = pack_bf16x2(fmaf(static_cast<float>(q[2 * i]), s, b),
-                       fmaf(static_cast<float>(q[2 * i + 1]), s, b));
-  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-  const u32x4v a = {p[0], p[1], p[2], p[3]};
-  const u32x4v c = {p[4], p[5], p[6], p[7]};
-  lo = __builtin_bit_cast(bf16x8, a);
-  hi = __builtin_bit_cast(bf16x8, c);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 = 0x00020000: raw (untyped) dword access on gfx9-family parts
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
 }
 
-template <int BITS, int BM>
+// 32 codes -> four MFMA operands of 8 bf16 (w = q*s + b, fp32 then RNE).
+template <int BITS>
+__device__ __forceinline__ void unpack32(const uint32_t (&w)[BITS], float s, float b,
+                                         bf16x8 (&f)[4]) {
+  uint32_t q[32];
+  decode_codes<BITS, 32, BITS>(w, q);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      p[i] = pack_bf16x2(fmaf(static_cast<float>(q[8 * j + 2 * i]), s, b),
+                         fmaf(static_cast<float>(q[8 * j + 2 * i + 1]), s, b));
+    const v4u v = {p[0], p[1], p[2], p[3]};
+    f[j] = __builtin_bit_cast(bf16x8, v);
+  }
+}
+
+// Packed weights of one K step as loaded: 2 row blocks x one 32-code run, plus
+// the raw bf16 scale and bias bits (converted only when unpacked).
+template <int BITS>
+struct RawW {
+  uint32_t w[2][BITS];
+  uint32_t s[2], b[2];
+};
+
+template <int BITS, int BM, bool KTAIL>
 __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int gs,
-    int m_tiles, int n_tiles) {
-  constexpr int NW = BITS / 2;      // words per 16-code run
-  constexpr int MB = BM / 16;       // 16-token blocks per wave
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    int gs_log2, int m_tiles, int n_tiles) {
+  constexpr int MB = BM / 32;       // 32-token blocks per wave
   constexpr int XL = BM / 32;       // 16-byte activation loads per thread per K step
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kXPitch];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, g4 = lane >> 4;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g2 = lane >> 5;
 
   // ---- tile order: XCD-contiguous ranges, then groups of 8 token tiles ----
   const int tiles = m_tiles * n_tiles;
@@ -98,125 +133,177 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   const int n_tile = in_group / gsize;
   const int m0 = m_tile * BM, n0 = n_tile * kBN;
 
-  const int64_t W = static_cast<int64_t>(K) * BITS / 32;
-  const int G = K / gs;
+  const int WB = K / 32 * BITS * 4;  // packed row bytes
+  const int G = K >> gs_log2;
   const int nk = (K + kKS - 1) / kKS;
+  const int rows_m = min(BM, M - m0), rows_n = min(kBN, N - n0);
 
-  const uint32_t* wrow[4];
-  const uint16_t* srow[4];
-  const uint16_t* brow[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int n = min(n0 + wave * 64 + nb * 16 + l16, N - 1);
-    wrow[nb] = wq + n * W;
-    srow[nb] = scales + static_cast<int64_t>(n) * G;
-    brow[nb] = biases + static_cast<int64_t>(n) * G;
-  }
-  const int xc = (tid & 7) * 8;  // activation column handled by this thread
-  const uint16_t* xrow[XL];
-#pragma unroll
-  for (int i = 0; i < XL; ++i) {
-    const int m = min(m0 + (tid >> 3) + 32 * i, M - 1);
-    xrow[i] = x + static_cast<int64_t>(m) * K + xc;
-  }
+  // descriptors rebased at the tile so all offsets fit in 32 bits
+  const __amdgpu_buffer_rsrc_t xrs =
+      make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(rows_m) * K * 2);
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(reinterpret_cast<const char*>(wq) + static_cast<int64_t>(n0) * WB,
+                static_cast<uint32_t>(rows_n) * WB);
+  const __amdgpu_buffer_rsrc_t srs =
+      make_rsrc(scales + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
+  const __amdgpu_buffer_rsrc_t brs =
+      make_rsrc(biases + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
 
-  f32x4 acc[4][MB];
+  // per-lane byte offsets (rows clamped into the tile: every access is in range)
+  int wvo[2], svo[2];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int nb = 0; nb < 2; ++nb) {
+    const int r = min(wave * 64 + nb * 32 + l32, rows_n - 1);
+    wvo[nb] = r * WB + g2 * BITS * 4;
+    svo[nb] = r * G * 2 + ((32 * g2) >> gs_log2) * 2;
+  }
+  const int xc = (tid & 7) * 8;  // activation column staged by this thread
+  int xvo[XL];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < XL; ++i) xvo[i] = (min((tid >> 3) + 32 * i, rows_m - 1) * K + xc) * 2;
+
+  f32x16 acc[2][MB];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x16{};
 
   u32x4 xr[XL];
-  uint32_t wr[4][NW];
-  float sr[4], br[4];
 
+  auto load_w = [&](int kk, RawW<BITS>& r) {
+    int so = kk * (8 * BITS);                   // 2 runs of BITS words per step
+    int ss = ((kk * kKS) >> gs_log2) * 2;
+    if constexpr (KTAIL) {
+      // a half step at the end: lanes past K re-read the previous run (in range)
+      const bool past = kk * kKS + 32 * g2 >= K;
+      so -= past ? 4 * BITS : 0;
+      ss -= past ? (((32 * g2) >> gs_log2) * 2) : 0;
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      buf_load_words<BITS>(wrs, wvo[nb] + (KTAIL ? so : 0), KTAIL ? 0 : so, r.w[nb]);
+      r.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb] + (KTAIL ? ss : 0),
+                                                     KTAIL ? 0 : ss, 0);
+      r.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb] + (KTAIL ? ss : 0),
+                                                     KTAIL ? 0 : ss, 0);
+    }
+  };
   auto load_x = [&](int kk) {
-    const int k0 = kk * kKS;
-    const bool ok = k0 + xc < K;
+    if constexpr (!KTAIL) {
 #pragma unroll
-    for (int i = 0; i < XL; ++i)
-      xr[i] = ok ? *reinterpret_cast<const u32x4*>(xrow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < XL; ++i)
+        xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              xrs, xvo[i], kk * kKS * 2, 0));
+    } else {
+      const int col = min(kk * kKS, K - 8 - xc) * 2;
+#pragma unroll
+      for (int i = 0; i < XL; ++i)
+        xr[i] = __builtin_bit_cast(u32x4,
+                                   __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo[i] + col, 0, 0));
+    }
   };
-  auto store_x = [&](int buf) {
+  auto store_x = [&](int buf, int kk) {
+    const bool ok = !KTAIL || (kk * kKS + xc < K);
 #pragma unroll
-    for (int i = 0; i < XL; ++i)
-      *reinterpret_cast<u32x4a*>(&xs[buf][((tid >> 3) + 32 * i) * kXPitch + xc]) = xr[i];
+    for (int i = 0; i < XL; ++i) {
+      u32x4 v = xr[i];
+      if (KTAIL && !ok) v = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4a*>(&xs[buf][((tid >> 3) + 32 * i) * kXPitch + xc]) = v;
+    }
   };
-  auto load_w = [&](int kk) {
-    const int kc = kk * kKS + 16 * g4;
-    const bool ok = kc < K;
-    const int g = ok ? kc / gs : 0;
+  auto dequant = [&](int kk, const RawW<BITS>& r, bf16x8 (&wf)[2][4]) {
+    const bool ok = !KTAIL || (kk * kKS + 32 * g2 < K);
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      if (ok) {
-        load_chunk<NW>(wrow[nb] + (kc / 16) * NW, wr[nb]);
-        sr[nb] = bf16_to_f32(srow[nb][g]);
-        br[nb] = bf16_to_f32(brow[nb][g]);
-      } else {
+    for (int nb = 0; nb < 2; ++nb) {
+      float s = __uint_as_float(r.s[nb] << 16), b = __uint_as_float(r.b[nb] << 16);
+      if (KTAIL && !ok) {
+        s = 0.f;
+        b = 0.f;
+      }
+      unpack32<BITS>(r.w[nb], s, b, wf[nb]);
+    }
+  };
+  // One K step: MFMAs of step kk (operands wf + LDS buffer kk&1) with the
+  // unpacking of step kk+1 (raw `cur`) interleaved; the loads of step kk+2
+  // go out first, into `nxt`.
+  auto step = [&](int kk, const bf16x8 (&wf)[2][4], bf16x8 (&wn)[2][4], const RawW<BITS>& cur,
+                  RawW<BITS>& nxt) {
+    load_w(min(kk + 2, nk - 1), nxt);
+    dequant(min(kk + 1, nk - 1), cur, wn);
+    const uint16_t* xb = xs[kk & 1] + l32 * kXPitch + 32 * g2;
 #pragma unroll
-        for (int j = 0; j < NW; ++j) wr[nb][j] = 0u;
-        sr[nb] = 0.f;
-        br[nb] = 0.f;
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) {
+        const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xb + mb * 32 * kXPitch + 8 * sl);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[nb][sl], xv, acc[nb][mb], 0, 0, 0);
       }
     }
+    // schedule: weight loads first, then per 32-token block four LDS reads
+    // and 8 MFMAs, each MFMA followed by up to four VALU (the unpacking)
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * ((BITS + 3) / 4) + 4, 0);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    }
+    store_x((kk + 1) & 1, kk + 1);
+    load_x(min(kk + 2, nk - 1));
+    __syncthreads();
   };
 
+  // ---- prologue: step 0 staged and unpacked, step 1 in flight ----
+  RawW<BITS> ra, rb;
+  bf16x8 wa[2][4], wb[2][4];
+  load_w(0, ra);
   load_x(0);
-  load_w(0);
-  store_x(0);
+  store_x(0, 0);
+  dequant(0, ra, wa);
+  load_w(min(1, nk - 1), ra);
+  load_x(min(1, nk - 1));
   __syncthreads();
 
-  for (int kk = 0; kk < nk; ++kk) {
-    bf16x8 wf[4][2];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) unpack16<BITS, NW>(wr[nb], sr[nb], br[nb], wf[nb][0], wf[nb][1]);
-
-    const bool more = kk + 1 < nk;
-    if (more) {
-      load_x(kk + 1);
-      load_w(kk + 1);
-    }
-
-    const uint16_t* xb = xs[kk & 1] + l16 * kXPitch + 16 * g4;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(xb + mb * 16 * kXPitch);
-      const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(xb + mb * 16 * kXPitch + 8);
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nb][0], x0, acc[nb][mb], 0, 0, 0);
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nb][1], x1, acc[nb][mb], 0, 0, 0);
-    }
-
-    if (more) store_x((kk + 1) & 1);
-    __syncthreads();
+  // ---- main loop, unrolled by two so the register roles swap without copies ----
+  int kk = 0;
+  for (; kk + 1 < nk; kk += 2) {
+    step(kk, wa, wb, ra, rb);
+    step(kk + 1, wb, wa, rb, ra);
   }
+  if (kk < nk) step(kk, wa, wb, ra, rb);
 
-  // ---- epilogue: lane holds y[m, n..n+3] for one token m ----
+  // ---- epilogue: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3) for one token m ----
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int n = n0 + wave * 64 + nb * 16 + 4 * g4;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias) {
+  for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bv[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
-    }
+    for (int a = 0; a < 4; ++a) {
+      const int n = n0 + wave * 64 + nb * 32 + 8 * a + 4 * g2;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = m0 + mb * 16 + l16;
-      if (m >= M) continue;
-      uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
-      const f32x4 a = acc[nb][mb];
-      if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
-        const uint32_t lo = pack_bf16x2(a[0] + bv[0], a[1] + bv[1]);
-        const uint32_t hi = pack_bf16x2(a[2] + bv[2], a[3] + bv[3]);
-        *reinterpret_cast<u32x2*>(dst) = u32x2{lo, hi};
-      } else {
+        for (int r = 0; r < 4; ++r) bv[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
+      }
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) dst[r] = f32_to_bf16(a[r] + bv[r]);
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = m0 + mb * 32 + l32;
+        if (m >= M) continue;
+        uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
+        const f32x16 c = acc[nb][mb];
+        const float v0 = c[4 * a] + bv[0], v1 = c[4 * a + 1] + bv[1];
+        const float v2 = c[4 * a + 2] + bv[2], v3 = c[4 * a + 3] + bv[3];
+        if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+        } else {
+          const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) dst[r] = f32_to_bf16(v[r]);
+        }
       }
     }
   }
@@ -230,8 +317,13 @@ hipError_t run_qmm(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
   const int n_tiles = (N + kBN - 1) / kBN;
   const int tiles = m_tiles * n_tiles;
   const int grid = (tiles + 7) / 8 * 8;
-  qmm_kernel<BITS, BM><<<grid, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K, gs, m_tiles,
-                                                 n_tiles);
+  const int gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
+  if (K % kKS == 0)
+    qmm_kernel<BITS, BM, false><<<grid, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                          gs_log2, m_tiles, n_tiles);
+  else
+    qmm_kernel<BITS, BM, true><<<grid, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                         gs_log2, m_tiles, n_tiles);
   return hipGetLastError();
 }
 
@@ -248,7 +340,9 @@ hipError_t pick_bm(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 
 namespace detail {
 
-bool qmm_supports_bits(int bits) { return bits == 2 || bits == 4 || bits == 6 || bits == 8; }
+bool qmm_supports_bits(int bits) {
+  return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+}
 
 hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,
                       const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
@@ -256,6 +350,8 @@ hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,
   if (M == 0 || N == 0) return hipSuccess;
   switch (bits) {
     case 2: return pick_bm<2>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 3: return pick_bm<3>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    case 5: return pick_bm<5>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 4: return pick_bm<4>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 6: return pick_bm<6>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 8: return pick_bm<8>(x, M, K, wq, scales, biases, N, gs, bias, y, s);

@@ -70,12 +70,14 @@ def _as_words(w):
     raise ValueError(f"packed weights must be uint32 (got {w.dtype}).")
 
 
-def quantized(w, group_size=64, bits=4, *, mode="minmax"):
+def quantized(w, group_size=64, bits=4, *, mode="minmax", scales_dtype=None):
     """Quantize w [..., K] along its last axis -> (wq uint32, scales, biases).
 
-    scales/biases have w's dtype (float32 or bfloat16) and shape [..., K/group_size];
-    wq has shape [..., K*bits/32]. mode "minmax": scale=(max-min)/(2^bits-1),
-    bias=min; mode "mlx_edge": mlx's sign-aware edge quantizer.
+    scales/biases have w's dtype (float32 or bfloat16; `scales_dtype` overrides)
+    and shape [..., K/group_size]; wq has shape [..., K*bits/32]. Codes come
+    from the fp32 scale and bias, which are then rounded to the stored dtype.
+    mode "minmax": scale=(max-min)/(2^bits-1), bias=min; mode "mlx_edge":
+    mlx's sign-aware edge quantizer.
     """
     _check_bits_gs("quantize", bits, group_size)
     if w.ndim < 2:
@@ -96,12 +98,15 @@ def quantized(w, group_size=64, bits=4, *, mode="minmax"):
     w = _dense(w)
     lead = tuple(w.shape[:-1])
     rows = w.numel() // K if K else 0
+    sdt = w.dtype if scales_dtype is None else scales_dtype
+    if sdt not in _SB_DTYPES:
+        raise ValueError(f"[quantize] scales must be float32 or bfloat16 (got {sdt}).")
     wq = torch.empty(lead + (K * bits // 32,), dtype=torch.uint32, device=w.device)
-    scales = torch.empty(lead + (K // group_size,), dtype=w.dtype, device=w.device)
+    scales = torch.empty(lead + (K // group_size,), dtype=sdt, device=w.device)
     biases = torch.empty_like(scales)
-    dt = _SB_DTYPES[w.dtype]
-    _lib.check(_lib.lib().mxq_quantize(_ptr(w), dt, rows, K, group_size, bits, modes[mode],
-                                       _ptr(wq), _ptr(scales), _ptr(biases), dt, _stream(w)))
+    _lib.check(_lib.lib().mxq_quantize(_ptr(w), _SB_DTYPES[w.dtype], rows, K, group_size, bits,
+                                       modes[mode], _ptr(wq), _ptr(scales), _ptr(biases),
+                                       _SB_DTYPES[sdt], _stream(w)))
     return wq, scales, biases
 
 
