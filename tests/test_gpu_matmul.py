@@ -73,9 +73,12 @@ def test_qmv_row_counts_and_split(dev, O, N):
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
-def test_qmm_parity_bits_gs(dev, O, bits, gs):
-    M, N, K = 200, 288, 640
-    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits + gs, with_bias=True)
+@pytest.mark.parametrize("M,K", [(200, 768), (100, 1024), (200, 640)])
+def test_qmm_parity_bits_gs(dev, O, bits, gs, M, K):
+    """K % 256 == 0 runs the ring-pipelined kernel (256- and 128-token tiles);
+    K = 640 runs the two-deep kernel."""
+    N = 288
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits + gs + M, with_bias=True)
     y = run(dev, x, wq, s, b, bias, gs, bits, path="qmm")
     assert_tight(y, O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias), f"qmm {bits}/{gs}")
     exact = O.qmm_f64(x, wq, s, b, gs, bits, bias=bias)

@@ -61,6 +61,17 @@ __device__ __forceinline__ uint32_t code_of(const uint32_t (&w)[NW]) {
   }
 }
 
+// Same as code_of with the index as a value: used inside fully unrolled loops,
+// where `i` folds to a constant (so `w` stays in registers).
+template <int BITS, int NW>
+__device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[NW], int i) {
+  const int p = i * BITS;
+  const int wd = p >> 5, off = p & 31;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  if (off + BITS <= 32) return (w[wd] >> off) & MASK;
+  return __builtin_amdgcn_alignbit(w[wd + 1], w[wd], off) & MASK;
+}
+
 template <int BITS, int NCODES, int NW, int I = 0>
 __device__ __forceinline__ void decode_codes(const uint32_t (&w)[NW], uint32_t (&q)[NCODES]) {
   if constexpr (I < NCODES) {

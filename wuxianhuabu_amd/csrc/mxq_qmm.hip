@@ -24,6 +24,8 @@
 // (BITS whole words, for every supported width) and reads 64 contiguous
 // activation bytes. The loop is software-pipelined: packed weights for step
 // k+2 are loaded and step k+1 is unpacked while step k's MFMAs run.
+#include <type_traits>
+
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
 
@@ -309,31 +311,324 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Ring-pipelined variant for K % 64 == 0 (every DiT projection shape).
+//
+// Latency is hidden by distance, since each SIMD runs a single wave:
+//   * activations go HBM -> LDS directly (buffer_load_dwordx4 ... lds, no
+//     VGPRs) into a 4-stage ring; step k+3 is requested while step k computes;
+//   * packed weights go HBM -> VGPRs into a 4-slot ring; step k+3 is requested
+//     while step k+1 is unpacked under step k's MFMAs;
+//   * the LDS fragments of 32-token block b+1 are read while block b's MFMAs
+//     issue.
+// LDS rows are 128 B (64 bf16) with the 16-byte chunks XOR-swizzled by
+// swz(r) = (r & 7) ^ ((r >> 3) & 1), so both the fragment reads (32 rows, same
+// logical chunk) and the staging writes are bank-conflict free.
+// ---------------------------------------------------------------------------
+constexpr int kXStages = 4;
+constexpr int kWSlots = 4;
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// 16 bytes per lane from the buffer straight into LDS at dst + 16*lane
+// (buffer_load_dwordx4 ... lds; dst must be wave-uniform).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* dst, int voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+// vmcnt-only wait (expcnt and lgkmcnt left at their maxima) for gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the ring: this wave's LDS-direct loads for the next
+// stage have landed (vmcnt(N), later requests stay in flight) and its LDS
+// reads are done (lgkmcnt(0)), then s_barrier. __syncthreads() would also wait
+// for every outstanding global load (vmcnt(0)), emptying the prefetch ring.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  wait_vmcnt<N>();
+  __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int BITS>
+struct RunLoads {  // VMEM instructions per 32-code run load
+  static constexpr int value = BITS == 5 || BITS == 6 || BITS == 8 ? 2 : 1;
+};
+
 template <int BITS, int BM>
-hipError_t run_qmm(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
-                   const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
-                   hipStream_t s) {
-  const int m_tiles = (M + BM - 1) / BM;
-  const int n_tiles = (N + kBN - 1) / kBN;
+__global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    int gs_log2, int m_tiles, int n_tiles) {
+  constexpr int MB = BM / 32;            // 32-token blocks per wave
+  constexpr int XL = BM / 32;            // LDS-direct loads per wave per K step (8 rows each)
+  constexpr int STAGE = BM * 64;         // bf16 elements per LDS stage
+  constexpr int WLOADS = 2 * (RunLoads<BITS>::value + 2);  // per K step per lane
+  constexpr int LOADS_PER_STEP = WLOADS + XL;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kXStages * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g2 = lane >> 5;
+
+  // ---- tile order: XCD-contiguous ranges, then groups of 8 token tiles ----
   const int tiles = m_tiles * n_tiles;
-  const int grid = (tiles + 7) / 8 * 8;
-  const int gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
-  if (K % kKS == 0)
-    qmm_kernel<BITS, BM, false><<<grid, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
-                                                          gs_log2, m_tiles, n_tiles);
-  else
-    qmm_kernel<BITS, BM, true><<<grid, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
-                                                         gs_log2, m_tiles, n_tiles);
+  int bid = blockIdx.x;
+  const int nblk = gridDim.x;  // padded to a multiple of 8 by the launcher
+  bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  if (bid >= tiles) return;
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * n_tiles;
+  const int first_m = (bid / per_group) * GROUP_M;
+  const int gsize = min(m_tiles - first_m, GROUP_M);
+  const int in_group = bid % per_group;
+  const int m_tile = first_m + in_group % gsize;
+  const int n_tile = in_group / gsize;
+  const int m0 = m_tile * BM, n0 = n_tile * kBN;
+
+  const int WB = K / 32 * BITS * 4;  // packed row bytes
+  const int G = K >> gs_log2;
+  const int nk = K / kKS;
+  const int rows_m = min(BM, M - m0), rows_n = min(kBN, N - n0);
+
+  const __amdgpu_buffer_rsrc_t xrs =
+      make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(rows_m) * K * 2);
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(reinterpret_cast<const char*>(wq) + static_cast<int64_t>(n0) * WB,
+                static_cast<uint32_t>(rows_n) * WB);
+  const __amdgpu_buffer_rsrc_t srs =
+      make_rsrc(scales + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
+  const __amdgpu_buffer_rsrc_t brs =
+      make_rsrc(biases + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
+
+  int wvo[2], svo[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int r = min(wave * 64 + nb * 32 + l32, rows_n - 1);
+    wvo[nb] = r * WB + g2 * BITS * 4;
+    svo[nb] = r * G * 2 + ((32 * g2) >> gs_log2) * 2;
+  }
+  // staging: instruction i of this wave fills LDS rows (wave*XL + i)*8 .. +8;
+  // lane t writes physical chunk t%8 of row +t/8 with logical chunk ^ swz(row)
+  int xvo[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int r = (wave * XL + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz(r);
+    xvo[i] = (min(r, rows_m - 1) * K + 8 * c) * 2;
+  }
+  // fragment reads: row mb*32 + l32, logical chunk 4*g2 + sl
+  int xro[4];
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) xro[sl] = l32 * 128 + (((4 * g2 + sl) ^ swz(l32)) * 16);
+
+  f32x16 acc[2][MB];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x16{};
+
+  auto load_w = [&](int kk, RawW<BITS>& r) {
+    const int so = kk * (8 * BITS);
+    const int ss = ((kk * kKS) >> gs_log2) * 2;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      buf_load_words<BITS>(wrs, wvo[nb], so, r.w[nb]);
+      r.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
+      r.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+    }
+  };
+  auto load_x = [&](int kk, int stage) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      uint16_t* dst = xs + stage * STAGE + (wave * XL + i) * 512;
+      lds_load16(xrs, dst, xvo[i], kk * kKS * 2);
+    }
+  };
+  auto read_frags = [&](int stage, int mb, bf16x8 (&f)[4]) {
+    const char* base = reinterpret_cast<const char*>(xs + stage * STAGE) + mb * 32 * 128;
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) f[sl] = *reinterpret_cast<const bf16x8*>(base + xro[sl]);
+  };
+
+  RawW<BITS> rw[kWSlots];
+  uint32_t wu[2][2][16];  // unpacked bf16 pairs: [buffer][row block][dword]
+
+  // One K step. J = kk mod 4 picks the register/LDS slots at compile time.
+  // Source order is the schedule (sched_barrier fences keep it): per 32-token
+  // block, the next block's LDS reads, then four pairs of MFMAs each followed
+  // by one 2-code slice of the next step's unpacking.
+  auto step = [&](auto Jc, int kk) {
+    constexpr int J = decltype(Jc)::value;
+    constexpr int XS = J % kXStages;        // stage holding step kk
+    constexpr int F = J % 2, FN = (J + 1) % 2;
+    const RawW<BITS>& nr = rw[(J + 1) % kWSlots];
+    // requests for step kk+3 (clamped; a repeated request is harmless)
+    const int kl = min(kk + 3, nk - 1);
+    load_w(kl, rw[(J + 3) % kWSlots]);
+    load_x(kl, (J + 3) % kXStages);
+    const float s0 = __uint_as_float(nr.s[0] << 16), b0 = __uint_as_float(nr.b[0] << 16);
+    const float s1 = __uint_as_float(nr.s[1] << 16), b1 = __uint_as_float(nr.b[1] << 16);
+    bf16x8 xa[4], xb[4];
+    read_frags(XS, 0, xa);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      bf16x8 (&cur)[4] = (mb & 1) ? xb : xa;
+      bf16x8 (&nxt)[4] = (mb & 1) ? xa : xb;
+      if (mb + 1 < MB) read_frags(XS, mb + 1, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const bf16x8 wv = __builtin_bit_cast(
+              bf16x8, v4u{wu[F][nb][4 * sl], wu[F][nb][4 * sl + 1], wu[F][nb][4 * sl + 2],
+                          wu[F][nb][4 * sl + 3]});
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, cur[sl], acc[nb][mb], 0, 0, 0);
+        }
+        // slices: (MB * 4) slots cover the 32 dwords of the next step's operands
+        constexpr int SLOTS = MB * 4;
+#pragma unroll
+        for (int d = (mb * 4 + sl) * 32 / SLOTS; d < (mb * 4 + sl + 1) * 32 / SLOTS; ++d) {
+          const int nb = d / 16, i = d % 16;
+          const float sc = nb ? s1 : s0, bi = nb ? b1 : b0;
+          wu[FN][nb][i] = pack_bf16x2(
+              fmaf(static_cast<float>(code_at<BITS>(nr.w[nb], 2 * i)), sc, bi),
+              fmaf(static_cast<float>(code_at<BITS>(nr.w[nb], 2 * i + 1)), sc, bi));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // the stage of step kk+1 was requested two steps ago: wait for this wave's
+    // part of it (everything issued later may stay in flight), then publish
+    ring_barrier<2 * LOADS_PER_STEP>();
+  };
+
+  // ---- prologue: steps 0..2 requested, step 0 unpacked ----
+  load_w(0, rw[0]);
+  load_x(0, 0);
+  load_w(min(1, nk - 1), rw[1]);
+  load_x(min(1, nk - 1), 1);
+  load_w(min(2, nk - 1), rw[2]);
+  load_x(min(2, nk - 1), 2);
+  {
+    const float s0 = __uint_as_float(rw[0].s[0] << 16), b0 = __uint_as_float(rw[0].b[0] << 16);
+    const float s1 = __uint_as_float(rw[0].s[1] << 16), b1 = __uint_as_float(rw[0].b[1] << 16);
+#pragma unroll
+    for (int d = 0; d < 32; ++d) {
+      const int nb = d / 16, i = d % 16;
+      const float sc = nb ? s1 : s0, bi = nb ? b1 : b0;
+      wu[0][nb][i] = pack_bf16x2(fmaf(static_cast<float>(code_at<BITS>(rw[0].w[nb], 2 * i)), sc, bi),
+                                 fmaf(static_cast<float>(code_at<BITS>(rw[0].w[nb], 2 * i + 1)), sc, bi));
+    }
+  }
+  ring_barrier<2 * LOADS_PER_STEP>();
+
+  int kk = 0;
+  for (; kk + 4 <= nk; kk += 4) {
+    step(std::integral_constant<int, 0>{}, kk);
+    step(std::integral_constant<int, 1>{}, kk + 1);
+    step(std::integral_constant<int, 2>{}, kk + 2);
+    step(std::integral_constant<int, 3>{}, kk + 3);
+  }
+  if (kk < nk) step(std::integral_constant<int, 0>{}, kk);
+  if (kk + 1 < nk) step(std::integral_constant<int, 1>{}, kk + 1);
+  if (kk + 2 < nk) step(std::integral_constant<int, 2>{}, kk + 2);
+
+  // ---- epilogue: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3) for one token m ----
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int n = n0 + wave * 64 + nb * 32 + 8 * a + 4 * g2;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bv[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = m0 + mb * 32 + l32;
+        if (m >= M) continue;
+        uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
+        const f32x16 c = acc[nb][mb];
+        const float v0 = c[4 * a] + bv[0], v1 = c[4 * a + 1] + bv[1];
+        const float v2 = c[4 * a + 2] + bv[2], v3 = c[4 * a + 3] + bv[3];
+        if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+        } else {
+          const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) dst[r] = f32_to_bf16(v[r]);
+        }
+      }
+    }
+  }
+}
+
+// Launch geometry shared by both kernels.
+struct Grid {
+  int m_tiles, n_tiles, blocks, gs_log2;
+};
+
+inline Grid grid_for(int M, int N, int BM, int gs) {
+  Grid g;
+  g.m_tiles = (M + BM - 1) / BM;
+  g.n_tiles = (N + kBN - 1) / kBN;
+  g.blocks = (g.m_tiles * g.n_tiles + 7) / 8 * 8;  // whole XCD rounds
+  g.gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
+  return g;
+}
+
+template <int BITS, int BM>
+hipError_t run_ring(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                    hipStream_t s) {
+  const Grid g = grid_for(M, N, BM, gs);
+  qmm_ring_kernel<BITS, BM><<<g.blocks, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                          g.gs_log2, g.m_tiles, g.n_tiles);
   return hipGetLastError();
 }
 
+template <int BITS, int BM>
+hipError_t run_step(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                    hipStream_t s) {
+  const Grid g = grid_for(M, N, BM, gs);
+  if (K % kKS == 0)
+    qmm_kernel<BITS, BM, false><<<g.blocks, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                              g.gs_log2, g.m_tiles, g.n_tiles);
+  else
+    qmm_kernel<BITS, BM, true><<<g.blocks, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                             g.gs_log2, g.m_tiles, g.n_tiles);
+  return hipGetLastError();
+}
+
+// K a multiple of 256 (every DiT projection): ring kernel with 256- or
+// 128-token tiles. Otherwise (a K tail of 64/128/192 codes, or a half step):
+// the two-deep kernel with tiles of at most 128 tokens.
 template <int BITS>
 hipError_t pick_bm(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
                    hipStream_t s) {
-  if (M <= 64) return run_qmm<BITS, 64>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
-  if (M <= 128) return run_qmm<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
-  return run_qmm<BITS, 256>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (K % (kKS * kXStages) == 0 && M > 64) {
+    if (M <= 128) return run_ring<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+    return run_ring<BITS, 256>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  }
+  if (M <= 64) return run_step<BITS, 64>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  return run_step<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
 }
 
 }  // namespace
