@@ -116,6 +116,38 @@ int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
             const void* biases, int64_t N, int group_size, int bits, const void* bias,
             void* y, mxq_stream stream);
 
+/* ---- tiled weight layout ----------------------------------------------------
+ * A load-time reordering of the same packed bits (no requantization) in which
+ * every weight load of both kernels is a coalesced 16-byte-per-lane access:
+ * records of (64 output rows x 64 codes) in row-block-major order, each record
+ * holding the codes in lane order followed by one (scale, bias) bf16 pair per
+ * lane unit. Rows past N are zero. Requires K % 64 == 0 and bf16 scales/biases.
+ * The MLX-layout entry points above remain the drop-in operators; the tiled
+ * ones are what QuantizedLinear uses once its weights are resident (the
+ * reference keeps weights resident the same way: H3Weights / MfLinear.load,
+ * `model/minimax h3/H3Common.swift:312-338`). No reference counterpart exists
+ * for the layout itself. */
+
+/* Bytes needed for the tiled copy of an N x K weight; negative on invalid
+ * arguments (then mxq_last_error() says why). */
+int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits);
+
+/* MLX layout (wq, scales, biases; bf16 scales/biases) -> tiled layout. */
+int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
+             int group_size, int bits, void* tiled, mxq_stream stream);
+
+/* mxq_quantized_matmul on tiled weights: GEMV for M <= MXQ_QMV_MAX_M, else
+ * the MFMA kernel. Same arithmetic and results as the MLX-layout paths. */
+int mxq_quantized_matmul_tiled(const void* x, int64_t M, int64_t K, const void* tiled,
+                               int64_t N, int group_size, int bits, const void* bias, void* y,
+                               mxq_stream stream);
+
+/* The two halves of mxq_quantized_matmul_tiled, callable directly. */
+int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                  int group_size, int bits, const void* bias, void* y, mxq_stream stream);
+int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                  int group_size, int bits, const void* bias, void* y, mxq_stream stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* mxq_last_error(void);
 

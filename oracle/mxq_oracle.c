@@ -163,6 +163,61 @@ int orc_unpack(const uint32_t* wq, int64_t N, int64_t K, int bits, uint8_t* code
 }
 
 /* ------------------------------------------------------------------------ */
+/* tiled layout                                                              */
+/* ------------------------------------------------------------------------ */
+
+int64_t orc_tiled_bytes(int64_t N, int64_t K, int gs, int bits) {
+  if (N < 0 || K < 0 || K % 64 != 0 || (gs != 32 && gs != 64 && gs != 128)) return -1;
+  if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8) return -1;
+  int64_t rec = 512 * (int64_t)bits + 256 * (gs == 32 ? 2 : 1);
+  return (N + 63) / 64 * (K / 64) * rec;
+}
+
+/* byte offset, inside a record, of word j of unit u in half h */
+static int64_t tiled_word_offset(int bits, int h, int u, int j) {
+  int64_t half = (int64_t)h * 256 * bits;
+  int full = bits / 4, rem = bits % 4;
+  if (j < 4 * full) return half + (j / 4) * 1024 + u * 16 + (j % 4) * 4;
+  return half + full * 1024 + u * 4 * rem + (j - 4 * full) * 4;
+}
+
+int orc_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int64_t N,
+             int64_t K, int gs, int bits, uint8_t* out) {
+  int64_t total = orc_tiled_bytes(N, K, gs, bits);
+  if (total < 0) return -1;
+  memset(out, 0, (size_t)total);
+  const int64_t nk = K / 64, W = K * bits / 32, G = K / gs;
+  const int64_t rec = 512 * (int64_t)bits + 256 * (gs == 32 ? 2 : 1);
+  const int gps = gs == 32 ? 2 : 1;
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t rb = n / 64;
+    const int h = (int)((n % 64) / 32), r = (int)(n % 32);
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t kk = k / 64;
+      const int g = (int)((k % 64) / 32);
+      const int u = r + 32 * g;
+      uint8_t* R = out + (rb * nk + kk) * rec;
+      uint32_t q = code_at(wq + n * W, k, bits);
+      for (int t = 0; t < bits; ++t) {
+        int pos = (int)(k % 32) * bits + t; /* bit position in the unit's run */
+        uint32_t* word = (uint32_t*)(R + tiled_word_offset(bits, h, u, pos / 32));
+        *word |= ((q >> t) & 1u) << (pos % 32);
+      }
+      if (k % gs == 0 || k % 32 == 0) {
+        /* the dword for (row, code half) names the group holding its codes */
+        int entry = (h * 32 + r) * gps + (gps == 2 ? g : 0);
+        if (gps == 2 || g == 0) {
+          uint32_t* e = (uint32_t*)(R + 512 * (int64_t)bits) + entry;
+          int64_t grp = k / gs;
+          *e = (uint32_t)scales[n * G + grp] | ((uint32_t)biases[n * G + grp] << 16);
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* quantizers                                                                */
 /* ------------------------------------------------------------------------ */
 

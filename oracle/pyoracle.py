@@ -65,6 +65,10 @@ def lib():
                                   _int, _vp, _i64, _int, _u16p]
     L.orc_qmm_mlx_cpu.restype = _int
     L.orc_gelu_tanh_bf16.argtypes = [_u16p, _i64, _u16p]
+    L.orc_tiled_bytes.argtypes = [_i64, _i64, _int, _int]
+    L.orc_tiled_bytes.restype = _i64
+    L.orc_tile.argtypes = [_u32p, _u16p, _u16p, _i64, _i64, _int, _int, _u8p]
+    L.orc_tile.restype = _int
     _lib = L
     return L
 
@@ -128,6 +132,22 @@ def unpack(wq, K, bits):
     codes = np.empty((N, K), np.uint8)
     _check(lib().orc_unpack(wq, N, K, bits, codes), "unpack")
     return codes
+
+
+def tiled_bytes(N, K, gs, bits):
+    return int(lib().orc_tiled_bytes(N, K, gs, bits))
+
+
+def tile(wq, scales, biases, K, gs, bits):
+    """MLX-layout triple (bf16 bits for scales/biases) -> tiled bytes (uint8)."""
+    wq = _c(wq, np.uint32)
+    N = wq.shape[0]
+    nbytes = tiled_bytes(N, K, gs, bits)
+    _check(0 if nbytes >= 0 else -1, "tiled_bytes")
+    out = np.empty(nbytes, np.uint8)
+    _check(lib().orc_tile(wq, _c(scales, np.uint16), _c(biases, np.uint16), N, K, gs, bits,
+                          out), "tile")
+    return out
 
 
 # ---- quantizer / dequant -----------------------------------------------------

@@ -101,6 +101,27 @@ def test_quantize_and_dequantize_validation(mxq_lib):
     assert L.mxq_unpack(f, 1, 32, 7, f, None) == _lib.MXQ_ERR_INVALID
 
 
+def test_tiled_validation(mxq_lib):
+    L = mxq_lib
+    f = _fake()
+    assert L.mxq_tiled_bytes(16384, 4096, 64, 6) == 256 * 64 * (512 * 6 + 256)
+    assert L.mxq_tiled_bytes(100, 256, 32, 3) == 2 * 4 * (512 * 3 + 512)
+    assert L.mxq_tiled_bytes(64, 96, 32, 4) == _lib.MXQ_ERR_INVALID   # K % 64
+    assert b"multiple of 64" in L.mxq_last_error()
+    assert L.mxq_tiled_bytes(64, 128, 64, 7) == _lib.MXQ_ERR_INVALID
+    assert L.mxq_tile(None, f, f, 64, 128, 64, 4, f, None) == _lib.MXQ_ERR_NULL
+    assert L.mxq_tile(None, None, None, 0, 128, 64, 4, None, None) == _lib.MXQ_OK
+    for fn in (L.mxq_qmm_tiled, L.mxq_qmv_tiled, L.mxq_quantized_matmul_tiled):
+        assert fn(f, 2, 96, f, 64, 32, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+        assert fn(f, 2, 128, f, 64, 64, 5 + 2, None, f, None) == _lib.MXQ_ERR_INVALID
+        assert fn(f, 2, 128, None, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_NULL
+        assert fn(None, 0, 128, None, 64, 64, 4, None, None, None) == _lib.MXQ_OK
+    # the tiled buffer must be 16-byte aligned (the kernels read it with b128 loads)
+    odd = ctypes.c_void_p(f.value + 4)
+    assert L.mxq_qmm_tiled(f, 2, 128, odd, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_ALIGNMENT
+    assert L.mxq_qmv_tiled(f, 9, 128, f, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+
+
 def test_errors_are_thread_local(mxq_lib):
     import threading
     assert _qmm(mxq_lib, bits=7) == _lib.MXQ_ERR_INVALID

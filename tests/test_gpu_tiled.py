@@ -1,0 +1,161 @@
+"""Tiled weight layout on the GPU: the tiler against the oracle's writer, and
+the tiled kernels against the MLX-layout kernels and the fp64 oracle.
+
+Tolerances: the tiled MFMA kernel shares every arithmetic step with the
+MLX-layout MFMA kernel (only where the weight bits are fetched from differs),
+so for M > 64 and K % 64 == 0 (where the MLX-layout path runs the same kernel)
+the outputs must be bit-identical. Elsewhere the tight bound of
+tests/gpu_util.assert_tight applies against the oracle (orc_qmm_f64_bf16w for
+the MFMA kernels, orc_qmm_f64 for the GEMV), and max|y - r| / max|r| <= 2e-2
+against the exact fp64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import wuxianhuabu_amd as mx
+from tests.gpu_util import (assert_tight, dev_bf16, dev_words, host_bf16, host_f32_of_bf16,
+                            spec_metric)
+from tests.test_gpu_matmul import make_case
+
+pytestmark = pytest.mark.gpu
+
+BITS = [2, 3, 4, 5, 6, 8]
+GS = [32, 64, 128]
+
+
+def _tile(dev, wq, s, b, gs, bits):
+    return mx.tile(dev_words(wq, dev), dev_bf16(s, dev), dev_bf16(b, dev), gs, bits)
+
+
+def _tiled_run(dev, x, tw, bias, path="auto"):
+    y = mx.tiled_matmul(dev_bf16(x, dev), tw,
+                        bias=None if bias is None else dev_bf16(bias, dev), path=path)
+    return y
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
+def test_tile_matches_oracle_bytes(dev, O, bits, gs):
+    N, K = 100, 384
+    _, wq, s, b, _ = make_case(O, 1, N, K, gs, bits, seed=bits * 7 + gs)
+    tw = _tile(dev, wq, s, b, gs, bits)
+    ref = O.tile(wq, s, b, K, gs, bits)
+    got = tw.data.cpu().numpy()
+    assert got.shape == ref.shape
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_tile_full_size_matches_oracle(dev, O):
+    """The benchmark weight geometry (16384 x 4096, 6-bit, gs 64)."""
+    N, K, gs, bits = 16384, 4096, 64, 6
+    rng = np.random.default_rng(7)
+    wq = rng.integers(0, 2 ** 32, size=(N, K * bits // 32), dtype=np.uint32)
+    s = rng.integers(0, 2 ** 16, size=(N, K // gs), dtype=np.uint16)
+    b = rng.integers(0, 2 ** 16, size=(N, K // gs), dtype=np.uint16)
+    tw = _tile(dev, wq, s, b, gs, bits)
+    np.testing.assert_array_equal(tw.data.cpu().numpy(), O.tile(wq, s, b, K, gs, bits))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
+@pytest.mark.parametrize("M,K", [(200, 768), (100, 1024), (300, 640)])
+def test_tiled_qmm_bit_identical_to_mlx_layout(dev, O, bits, gs, M, K):
+    N = 288
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 31 + gs + K,
+                                  with_bias=(bits % 2 == 0))
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y_t = _tiled_run(dev, x, tw, bias, path="qmm")
+    y_m = mx.quantized_matmul(dev_bf16(x, dev), dev_words(wq, dev), dev_bf16(s, dev),
+                              dev_bf16(b, dev), group_size=gs, bits=bits,
+                              bias=None if bias is None else dev_bf16(bias, dev), path="qmm")
+    np.testing.assert_array_equal(host_bf16(y_t), host_bf16(y_m))
+    rows = np.arange(0, M, 7)
+    ref = O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows)
+    assert_tight(host_f32_of_bf16(y_t)[rows], ref, f"tiled qmm bits={bits} gs={gs}")
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 64, 64), (33, 1, 128), (64, 130, 192), (65, 200, 320),
+                                   (129, 63, 256), (257, 300, 512), (1000, 100, 1088)])
+def test_tiled_qmm_shapes(dev, O, M, N, K):
+    gs, bits = 64, 6
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=M + N + K, with_bias=True)
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y = host_f32_of_bf16(_tiled_run(dev, x, tw, bias, path="qmm"))
+    assert_tight(y, O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias),
+                 f"tiled qmm M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+def test_tiled_qmv_parity(dev, O, bits, gs, M):
+    N, K = 200, 512
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 100 + gs + M + 1,
+                                  with_bias=(M % 2 == 1))
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y = host_f32_of_bf16(_tiled_run(dev, x, tw, bias, path="qmv"))
+    ref = O.qmm_f64(x, wq, s, b, gs, bits, bias=bias)
+    assert_tight(y, ref, f"tiled qmv bits={bits} gs={gs} M={M}")
+    assert spec_metric(y, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("N,K", [(1, 64), (63, 128), (65, 4096), (24576 // 8, 4096),
+                                 (300, 11264)])
+def test_tiled_qmv_shapes(dev, O, N, K):
+    M, gs, bits = 2, 64, 6
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=N + K, with_bias=True)
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y = host_f32_of_bf16(_tiled_run(dev, x, tw, bias, path="qmv"))
+    assert_tight(y, O.qmm_f64(x, wq, s, b, gs, bits, bias=bias), f"tiled qmv N={N} K={K}")
+
+
+def test_tiled_dispatch_boundary(dev, O):
+    """M = 8 runs the GEMV, M = 9 the MFMA kernel; both agree with the oracle."""
+    N, K, gs, bits = 130, 512, 64, 4
+    for M in (8, 9):
+        x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=M)
+        tw = _tile(dev, wq, s, b, gs, bits)
+        y = host_f32_of_bf16(_tiled_run(dev, x, tw, bias))
+        ref = O.qmm_f64(x, wq, s, b, gs, bits)
+        assert spec_metric(y, ref) <= 2e-2
+
+
+def test_tiled_leading_dims_and_errors(dev, O):
+    N, K, gs, bits = 64, 256, 64, 4
+    x, wq, s, b, _ = make_case(O, 6, N, K, gs, bits, seed=3)
+    tw = _tile(dev, wq, s, b, gs, bits)
+    x3 = dev_bf16(x, dev).reshape(2, 3, K)
+    y = mx.tiled_matmul(x3, tw)
+    assert tuple(y.shape) == (2, 3, N)
+    y0 = mx.tiled_matmul(torch.empty(0, K, dtype=torch.bfloat16, device=dev), tw)
+    assert tuple(y0.shape) == (0, N)
+    with pytest.raises(ValueError, match="does not match"):
+        mx.tiled_matmul(torch.zeros(2, K + 64, dtype=torch.bfloat16, device=dev), tw)
+    with pytest.raises(ValueError, match="bfloat16"):
+        mx.tiled_matmul(torch.zeros(2, K, dtype=torch.float32, device=dev), tw)
+    # K = 96 cannot be tiled (K % 64 != 0)
+    _, wq2, s2, b2, _ = make_case(O, 1, N, 96, 32, bits, seed=4)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _tile(dev, wq2, s2, b2, 32, bits)
+
+
+def test_quantized_linear_uses_tiled_copy(dev, O):
+    """The module's tiled call equals the MLX-layout operator bit for bit
+    (M > 64), and tiled=False runs the MLX-layout kernels."""
+    N, K, gs, bits, M = 192, 512, 64, 6, 130
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=77, with_bias=True)
+    args = (dev_words(wq, dev), dev_bf16(s, dev), dev_bf16(b, dev), dev_bf16(bias, dev))
+    lin = mx.QuantizedLinear.from_weights(*args, group_size=gs, bits=bits)
+    xd = dev_bf16(x, dev)
+    y = lin(xd)
+    assert lin.tiled_weight() is not None
+    ref = mx.quantized_matmul(xd, *args[:3], group_size=gs, bits=bits, bias=args[3])
+    assert torch.equal(y, ref)
+    plain = mx.QuantizedLinear.from_weights(*args, group_size=gs, bits=bits, tiled=False)
+    assert plain.tiled_weight() is None
+    assert torch.equal(plain(xd), ref)
+    # update() drops the stale tiled copy
+    lin.update({"weight": args[0], "scales": args[1], "biases": args[2]})
+    assert lin._tw is None
+    assert torch.equal(lin(xd), ref)

@@ -11,12 +11,13 @@ whose C ABI is include/mxq.h.
 """
 from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
 from .nn import MfLinear, QuantizedLinear  # noqa: F401
-from .ops import (dequantized, pack, quantized, quantized_matmul,  # noqa: F401
-                  quantizedMatmul, quantizedMM, unpack)
+from .ops import (TiledWeight, dequantized, pack, quantized, quantized_matmul,  # noqa: F401
+                  quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
 
 __all__ = [
     "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
-    "pack", "unpack", "QuantizedLinear", "MfLinear", "get_quantized", "infer_geometry",
+    "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight",
+    "QuantizedLinear", "MfLinear", "get_quantized", "infer_geometry",
     "header_candidates", "lib", "LIB_PATH", "MXQError",
 ]

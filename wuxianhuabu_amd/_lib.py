@@ -34,6 +34,12 @@ SIGNATURES = {
                                     _vp, _vp, _vp]),
     "mxq_qmm": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_qmv": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
+    "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),
+    "mxq_tile": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
+    "mxq_quantized_matmul_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp,
+                                          _vp]),
+    "mxq_qmm_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
+    "mxq_qmv_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_last_error": (ctypes.c_char_p, []),
     "mxq_status_string": (ctypes.c_char_p, [_int]),
     "mxq_stream_synchronize": (_int, [_vp]),

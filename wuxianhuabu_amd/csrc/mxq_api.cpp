@@ -16,6 +16,7 @@
 #include <cstring>
 
 #include "mxq_internal.hpp"
+#include "mxq_tiled.hpp"
 
 namespace {
 
@@ -234,6 +235,98 @@ int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
                     mxq::detail::launch_qmm(xb, static_cast<int>(M), static_cast<int>(K), wq, sc,
                                             bi, static_cast<int>(N), group_size, bits, bs, yb,
                                             s));
+}
+
+int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits) {
+  int rc = check_bits_gs("tile", bits, group_size, K);
+  if (rc) return rc;
+  if (N < 0) return fail(MXQ_ERR_INVALID, "[tile] N must be non-negative.");
+  if (K % 64 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[tile] The tiled layout needs K to be a multiple of 64 (got %lld).",
+                static_cast<long long>(K));
+  ok();
+  return mxq::tiled::total_bytes(N, K, group_size, bits);
+}
+
+int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
+             int group_size, int bits, void* tiled, mxq_stream stream) {
+  const int64_t bytes = mxq_tiled_bytes(N, K, group_size, bits);
+  if (bytes < 0) return static_cast<int>(bytes);
+  if (N == 0 || K == 0) return ok();
+  if (!wq || !scales || !biases || !tiled)
+    return fail(MXQ_ERR_NULL, "[tile] w, scales, biases and tiled must be non-NULL.");
+  if (!aligned4(wq) || !aligned4(scales) || !aligned4(biases) ||
+      (reinterpret_cast<uintptr_t>(tiled) & 15u) != 0)
+    return fail(MXQ_ERR_ALIGNMENT,
+                "[tile] w, scales and biases must be 4-byte aligned, tiled 16-byte aligned.");
+  return hip_status("tile", mxq::detail::launch_tile(
+                                wq, static_cast<const uint16_t*>(scales),
+                                static_cast<const uint16_t*>(biases), N, K, group_size, bits,
+                                tiled, static_cast<hipStream_t>(stream)));
+}
+
+namespace {
+int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void* tiled,
+                int64_t N, int gs, int bits, const void* bias, const void* y) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(MXQ_ERR_INVALID, "[%s] Negative dimension.", op);
+  int rc = check_bits_gs(op, bits, gs, K);
+  if (rc) return rc;
+  if (K == 0 || K % 64 != 0)
+    return fail(MXQ_ERR_INVALID, "[%s] Tiled weights need K to be a positive multiple of 64.",
+                op);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MXQ_ERR_INVALID, "[%s] Dimensions above 2^31-1 are not supported.", op);
+  if (mxq::tiled::total_bytes(N, K, gs, bits) / mxq::tiled::row_blocks(N == 0 ? 1 : N) >
+      INT32_MAX)
+    return fail(MXQ_ERR_INVALID, "[%s] K too large for one row block (%lld).", op,
+                static_cast<long long>(K));
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (!x || !tiled || !y) return fail(MXQ_ERR_NULL, "[%s] x, tiled and y must be non-NULL.", op);
+  if (!aligned4(x) || !aligned4(y) || (bias && !aligned4(bias)) ||
+      (reinterpret_cast<uintptr_t>(tiled) & 15u) != 0)
+    return fail(MXQ_ERR_ALIGNMENT,
+                "[%s] x, y and bias must be 4-byte aligned, tiled 16-byte aligned.", op);
+  return MXQ_OK;
+}
+}  // namespace
+
+int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                  int group_size, int bits, const void* bias, void* y, mxq_stream stream) {
+  int rc = check_tiled("quantized_matmul", x, M, K, tiled, N, group_size, bits, bias, y);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return ok();
+  return hip_status("quantized_matmul",
+                    mxq::detail::launch_qmm_tiled(
+                        static_cast<const uint16_t*>(x), static_cast<int>(M),
+                        static_cast<int>(K), tiled, static_cast<int>(N), group_size, bits,
+                        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                        static_cast<hipStream_t>(stream)));
+}
+
+int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                  int group_size, int bits, const void* bias, void* y, mxq_stream stream) {
+  int rc = check_tiled("quantized_matmul", x, M, K, tiled, N, group_size, bits, bias, y);
+  if (rc) return rc;
+  if (M > MXQ_QMV_MAX_M)
+    return fail(MXQ_ERR_INVALID, "[qmv] M=%lld exceeds the GEMV limit %d.",
+                static_cast<long long>(M), MXQ_QMV_MAX_M);
+  if (M == 0 || N == 0) return ok();
+  return hip_status("quantized_matmul",
+                    mxq::detail::launch_qmv_tiled(
+                        static_cast<const uint16_t*>(x), static_cast<int>(M),
+                        static_cast<int>(K), tiled, static_cast<int>(N), group_size, bits,
+                        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                        static_cast<hipStream_t>(stream)));
+}
+
+int mxq_quantized_matmul_tiled(const void* x, int64_t M, int64_t K, const void* tiled,
+                               int64_t N, int group_size, int bits, const void* bias, void* y,
+                               mxq_stream stream) {
+  if (M <= MXQ_QMV_MAX_M)
+    return mxq_qmv_tiled(x, M, K, tiled, N, group_size, bits, bias, y, stream);
+  return mxq_qmm_tiled(x, M, K, tiled, N, group_size, bits, bias, y, stream);
 }
 
 int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,

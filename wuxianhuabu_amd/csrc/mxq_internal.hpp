@@ -20,6 +20,10 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void*
                              int sb_dtype, int64_t rows, int64_t cols, int gs, int bits,
                              void* out, int out_dtype, hipStream_t s);
 
+// MLX layout -> tiled layout (mxq_tiled.hpp). K % 64 == 0, bf16 scales/biases.
+hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                       int64_t N, int64_t K, int gs, int bits, void* out, hipStream_t s);
+
 // y[M,N] = x[M,K] * W^T (+ bias): small-M split-K GEMV (any M; rows of x are
 // processed in blocks of up to 8).
 hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,
@@ -32,6 +36,13 @@ hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,
                       const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
                       const uint16_t* bias, uint16_t* y, hipStream_t s);
 bool qmm_supports_bits(int bits);
+
+// Both kernels on tiled weights (K % 64 == 0): any M for the MFMA kernel,
+// M <= 8 for the GEMV.
+hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
+                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
+hipError_t launch_qmv_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
+                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
 
 }  // namespace detail
 }  // namespace mxq

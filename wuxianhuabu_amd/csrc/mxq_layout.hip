@@ -12,6 +12,7 @@
 //                `model/minimax h3/H3Common.swift:389-394` (LSB-first codes)
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
+#include "mxq_tiled.hpp"
 
 namespace mxq {
 namespace {
@@ -158,6 +159,69 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint32_t* __
   for (int i = 0; i < PC; ++i) store_f32(dst + i, fmaf(static_cast<float>(q[i]), s, b));
 }
 
+// One thread per (row block, K step, half, unit): copies the unit's `BITS`
+// words into its planes and, for the unit that owns it, writes the
+// (scale, bias) pair. See mxq_tiled.hpp for the layout.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restrict__ wq,
+                                                        const uint16_t* __restrict__ scales,
+                                                        const uint16_t* __restrict__ biases,
+                                                        int64_t N, int64_t K, int gs,
+                                                        uint8_t* __restrict__ out) {
+  const int64_t nk = K / 64;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t items = tiled::row_blocks(N) * nk * 128;
+  if (idx >= items) return;
+  const int u = static_cast<int>(idx & 63);
+  const int h = static_cast<int>((idx >> 6) & 1);
+  const int64_t rk = idx >> 7;  // rb * nk + kk
+  const int64_t rb = rk / nk, kk = rk - rb * nk;
+  const int r = u & 31, g = u >> 5;
+  const int64_t row = rb * 64 + h * 32 + r;
+  const bool valid = row < N;
+  const int64_t W = K / 32 * BITS;
+  uint32_t words[BITS];
+  const uint32_t* src = wq + (valid ? row : 0) * W + (kk * 64 + 32 * g) / 32 * BITS;
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) words[i] = valid ? src[i] : 0u;
+  uint8_t* rec = out + rk * tiled::record_bytes(BITS, gs);
+  uint8_t* half = rec + h * tiled::half_bytes(BITS);
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+#pragma unroll
+  for (int p = 0; p < FP; ++p) {
+    uint32_t* d = reinterpret_cast<uint32_t*>(half + p * 1024 + u * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = words[4 * p + i];
+  }
+  if constexpr (RW > 0) {
+    uint32_t* d = reinterpret_cast<uint32_t*>(half + FP * 1024 + u * 4 * RW);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) d[i] = words[4 * FP + i];
+  }
+  const int G = tiled::gps(gs);
+  if (G == 2 || g == 0) {
+    const int64_t grp = (kk * 64 + 32 * g) / gs;
+    const int64_t si = (valid ? row : 0) * (K / gs) + grp;
+    const uint32_t sv = valid ? scales[si] : 0u;
+    const uint32_t bv = valid ? biases[si] : 0u;
+    uint32_t* e = reinterpret_cast<uint32_t*>(rec + tiled::code_bytes(BITS)) +
+                  ((h * 32 + r) * G + (G == 2 ? g : 0));
+    *e = sv | (bv << 16);
+  }
+}
+
+template <int BITS>
+struct TileRun {
+  static hipError_t run(const uint32_t* wq, const uint16_t* sc, const uint16_t* bi, int64_t N,
+                        int64_t K, int gs, void* out, hipStream_t s) {
+    const int64_t items = tiled::row_blocks(N) * (K / 64) * 128;
+    if (items == 0) return hipSuccess;
+    tile_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, sc, bi, N, K, gs,
+                                                           static_cast<uint8_t*>(out));
+    return hipGetLastError();
+  }
+};
+
 template <template <int> class F, typename... A>
 hipError_t by_bits(int bits, A... args) {
   switch (bits) {
@@ -263,6 +327,11 @@ hipError_t launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t col
                            int sb_dtype, hipStream_t s) {
   return by_bits<QuantizeRun>(bits, w, w_dtype, rows, cols, gs, mode, wq, scales, biases,
                               sb_dtype, s);
+}
+
+hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                       int64_t N, int64_t K, int gs, int bits, void* out, hipStream_t s) {
+  return by_bits<TileRun>(bits, wq, scales, biases, N, K, gs, out, s);
 }
 
 hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,

@@ -28,6 +28,7 @@
 
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
+#include "mxq_tiled.hpp"
 
 namespace mxq {
 namespace {
@@ -363,16 +364,18 @@ struct RunLoads {  // VMEM instructions per 32-code run load
   static constexpr int value = BITS == 5 || BITS == 6 || BITS == 8 ? 2 : 1;
 };
 
-template <int BITS, int BM>
+template <int BITS, int BM, bool TILED>
 __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
-    int gs_log2, int m_tiles, int n_tiles) {
+    const uint8_t* __restrict__ tw, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int M, int N, int K, int gs_log2, int m_tiles, int n_tiles) {
   constexpr int MB = BM / 32;            // 32-token blocks per wave
   constexpr int XL = BM / 32;            // LDS-direct loads per wave per K step (8 rows each)
   constexpr int STAGE = BM * 64;         // bf16 elements per LDS stage
-  constexpr int WLOADS = 2 * (RunLoads<BITS>::value + 2);  // per K step per lane
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  // weight VMEM instructions per K step per lane
+  constexpr int WLOADS = TILED ? 2 * (FP + (RW > 0 ? 1 : 0) + 1) : 2 * (RunLoads<BITS>::value + 2);
   constexpr int LOADS_PER_STEP = WLOADS + XL;
   __shared__ __attribute__((aligned(16))) uint16_t xs[kXStages * STAGE];
 
@@ -403,20 +406,35 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
 
   const __amdgpu_buffer_rsrc_t xrs =
       make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(rows_m) * K * 2);
-  const __amdgpu_buffer_rsrc_t wrs =
-      make_rsrc(reinterpret_cast<const char*>(wq) + static_cast<int64_t>(n0) * WB,
-                static_cast<uint32_t>(rows_n) * WB);
-  const __amdgpu_buffer_rsrc_t srs =
-      make_rsrc(scales + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
-  const __amdgpu_buffer_rsrc_t brs =
-      make_rsrc(biases + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
-
-  int wvo[2], svo[2];
+  // weights: MLX rows of this tile, or the tiled records of this wave's
+  // 64-row block (all offsets per lane fixed; the K step is a scalar offset)
+  const int gp = gs_log2 == 5 ? 2 : 1;
+  const int rs = TILED ? 512 * BITS + 256 * gp : 0;  // tiled record bytes
+  __amdgpu_buffer_rsrc_t wrs, srs, brs;
+  int wvo[2], rvo[2], svo[2];
+  if constexpr (TILED) {
+    const int rb = min((n0 >> 6) + wave, (N + 63) / 64 - 1);
+    wrs = make_rsrc(tw + static_cast<int64_t>(rb) * nk * rs, static_cast<uint32_t>(nk) * rs);
+    srs = wrs;
+    brs = wrs;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int r = min(wave * 64 + nb * 32 + l32, rows_n - 1);
-    wvo[nb] = r * WB + g2 * BITS * 4;
-    svo[nb] = r * G * 2 + ((32 * g2) >> gs_log2) * 2;
+    for (int nb = 0; nb < 2; ++nb) {
+      wvo[nb] = nb * tiled::half_bytes(BITS) + lane * 16;
+      rvo[nb] = nb * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
+      svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * gp + (gp == 2 ? g2 : 0)) * 4;
+    }
+  } else {
+    wrs = make_rsrc(reinterpret_cast<const char*>(wq) + static_cast<int64_t>(n0) * WB,
+                    static_cast<uint32_t>(rows_n) * WB);
+    srs = make_rsrc(scales + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
+    brs = make_rsrc(biases + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int r = min(wave * 64 + nb * 32 + l32, rows_n - 1);
+      wvo[nb] = r * WB + g2 * BITS * 4;
+      rvo[nb] = 0;
+      svo[nb] = r * G * 2 + ((32 * g2) >> gs_log2) * 2;
+    }
   }
   // staging: instruction i of this wave fills LDS rows (wave*XL + i)*8 .. +8;
   // lane t writes physical chunk t%8 of row +t/8 with logical chunk ^ swz(row)
@@ -439,14 +457,44 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x16{};
 
   auto load_w = [&](int kk, RawW<BITS>& r) {
-    const int so = kk * (8 * BITS);
-    const int ss = ((kk * kKS) >> gs_log2) * 2;
+    if constexpr (TILED) {
+      const int so = kk * rs;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      buf_load_words<BITS>(wrs, wvo[nb], so, r.w[nb]);
-      r.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
-      r.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int p = 0; p < FP; ++p) {
+          const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+          r.w[nb][4 * p] = v.x; r.w[nb][4 * p + 1] = v.y;
+          r.w[nb][4 * p + 2] = v.z; r.w[nb][4 * p + 3] = v.w;
+        }
+        if constexpr (RW == 1) {
+          r.w[nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+        } else if constexpr (RW == 2) {
+          const v2u v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
+          r.w[nb][4 * FP] = v.x; r.w[nb][4 * FP + 1] = v.y;
+        } else if constexpr (RW == 3) {
+          const v3u v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
+          r.w[nb][4 * FP] = v.x; r.w[nb][4 * FP + 1] = v.y; r.w[nb][4 * FP + 2] = v.z;
+        }
+        r.s[nb] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], so, 0);
+        r.b[nb] = 0u;
+      }
+    } else {
+      const int so = kk * (8 * BITS);
+      const int ss = ((kk * kKS) >> gs_log2) * 2;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        buf_load_words<BITS>(wrs, wvo[nb], so, r.w[nb]);
+        r.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
+        r.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+      }
     }
+  };
+  // scale and bias of row block nb from the raw bits (tiled: one dword, scale
+  // in the low half; MLX: two bf16 loads)
+  auto scale_bias = [&](const RawW<BITS>& r, int nb, float& sc, float& bi) {
+    sc = __uint_as_float(r.s[nb] << 16);
+    bi = TILED ? __uint_as_float(r.s[nb] & 0xFFFF0000u) : __uint_as_float(r.b[nb] << 16);
   };
   auto load_x = [&](int kk, int stage) {
 #pragma unroll
@@ -477,8 +525,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
     const int kl = min(kk + 3, nk - 1);
     load_w(kl, rw[(J + 3) % kWSlots]);
     load_x(kl, (J + 3) % kXStages);
-    const float s0 = __uint_as_float(nr.s[0] << 16), b0 = __uint_as_float(nr.b[0] << 16);
-    const float s1 = __uint_as_float(nr.s[1] << 16), b1 = __uint_as_float(nr.b[1] << 16);
+    float s0, b0, s1, b1;
+    scale_bias(nr, 0, s0, b0);
+    scale_bias(nr, 1, s1, b1);
+    // steps past K (the loop runs a multiple of 4 steps) only keep the
+    // request/barrier cadence
+    if (kk < nk) {
     bf16x8 xa[4], xb[4];
     read_frags(XS, 0, xa);
     __builtin_amdgcn_sched_barrier(0);
@@ -510,6 +562,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    }
     // the stage of step kk+1 was requested two steps ago: wait for this wave's
     // part of it (everything issued later may stay in flight), then publish
     ring_barrier<2 * LOADS_PER_STEP>();
@@ -523,8 +576,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
   load_w(min(2, nk - 1), rw[2]);
   load_x(min(2, nk - 1), 2);
   {
-    const float s0 = __uint_as_float(rw[0].s[0] << 16), b0 = __uint_as_float(rw[0].b[0] << 16);
-    const float s1 = __uint_as_float(rw[0].s[1] << 16), b1 = __uint_as_float(rw[0].b[1] << 16);
+    float s0, b0, s1, b1;
+    scale_bias(rw[0], 0, s0, b0);
+    scale_bias(rw[0], 1, s1, b1);
 #pragma unroll
     for (int d = 0; d < 32; ++d) {
       const int nb = d / 16, i = d % 16;
@@ -535,16 +589,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
   }
   ring_barrier<2 * LOADS_PER_STEP>();
 
-  int kk = 0;
-  for (; kk + 4 <= nk; kk += 4) {
+  for (int kk = 0; kk < nk; kk += 4) {
     step(std::integral_constant<int, 0>{}, kk);
     step(std::integral_constant<int, 1>{}, kk + 1);
     step(std::integral_constant<int, 2>{}, kk + 2);
     step(std::integral_constant<int, 3>{}, kk + 3);
   }
-  if (kk < nk) step(std::integral_constant<int, 0>{}, kk);
-  if (kk + 1 < nk) step(std::integral_constant<int, 1>{}, kk + 1);
-  if (kk + 2 < nk) step(std::integral_constant<int, 2>{}, kk + 2);
 
   // ---- epilogue: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3) for one token m ----
 #pragma unroll
@@ -592,13 +642,14 @@ inline Grid grid_for(int M, int N, int BM, int gs) {
   return g;
 }
 
-template <int BITS, int BM>
+template <int BITS, int BM, bool TILED>
 hipError_t run_ring(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
-                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
-                    hipStream_t s) {
+                    const uint16_t* bi, const void* tw, int N, int gs, const uint16_t* bias,
+                    uint16_t* y, hipStream_t s) {
   const Grid g = grid_for(M, N, BM, gs);
-  qmm_ring_kernel<BITS, BM><<<g.blocks, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
-                                                          g.gs_log2, g.m_tiles, g.n_tiles);
+  qmm_ring_kernel<BITS, BM, TILED><<<g.blocks, kThreads, 0, s>>>(
+      x, wq, sc, bi, static_cast<const uint8_t*>(tw), bias, y, M, N, K, g.gs_log2, g.m_tiles,
+      g.n_tiles);
   return hipGetLastError();
 }
 
@@ -616,16 +667,16 @@ hipError_t run_step(const uint16_t* x, int M, int K, const uint32_t* wq, const u
   return hipGetLastError();
 }
 
-// K a multiple of 256 (every DiT projection): ring kernel with 256- or
-// 128-token tiles. Otherwise (a K tail of 64/128/192 codes, or a half step):
-// the two-deep kernel with tiles of at most 128 tokens.
+// K a multiple of 64 (every DiT projection) and more than 64 tokens: ring
+// kernel with 256- or 128-token tiles. Otherwise (a half step at the end of K,
+// or few tokens): the two-deep kernel with tiles of at most 128 tokens.
 template <int BITS>
 hipError_t pick_bm(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
                    hipStream_t s) {
-  if (K % (kKS * kXStages) == 0 && M > 64) {
-    if (M <= 128) return run_ring<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
-    return run_ring<BITS, 256>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (K % kKS == 0 && M > 64) {
+    if (M <= 128) return run_ring<BITS, 128, false>(x, M, K, wq, sc, bi, nullptr, N, gs, bias, y, s);
+    return run_ring<BITS, 256, false>(x, M, K, wq, sc, bi, nullptr, N, gs, bias, y, s);
   }
   if (M <= 64) return run_step<BITS, 64>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
   return run_step<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
@@ -637,6 +688,28 @@ namespace detail {
 
 bool qmm_supports_bits(int bits) {
   return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+}
+
+template <int BITS>
+hipError_t pick_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
+                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M <= 128)
+    return run_ring<BITS, 128, true>(x, M, K, nullptr, nullptr, nullptr, tw, N, gs, bias, y, s);
+  return run_ring<BITS, 256, true>(x, M, K, nullptr, nullptr, nullptr, tw, N, gs, bias, y, s);
+}
+
+hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
+                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  switch (bits) {
+    case 2: return pick_tiled<2>(x, M, K, tw, N, gs, bias, y, s);
+    case 3: return pick_tiled<3>(x, M, K, tw, N, gs, bias, y, s);
+    case 4: return pick_tiled<4>(x, M, K, tw, N, gs, bias, y, s);
+    case 5: return pick_tiled<5>(x, M, K, tw, N, gs, bias, y, s);
+    case 6: return pick_tiled<6>(x, M, K, tw, N, gs, bias, y, s);
+    case 8: return pick_tiled<8>(x, M, K, tw, N, gs, bias, y, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,

@@ -17,6 +17,7 @@
 // so each weight costs one decode and MT fused multiply-adds.
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
+#include "mxq_tiled.hpp"
 
 namespace mxq {
 namespace {
@@ -223,6 +224,188 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
   return pick_split<BITS, 8>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
 }
 
+// ---------------------------------------------------------------------------
+// GEMV on the tiled layout (mxq_tiled.hpp). One workgroup per 64-row block;
+// its WPB waves split the block's K steps into contiguous ranges (the block's
+// records are contiguous in HBM, so each wave streams one span). Per step a
+// lane owns two units (rows r and r+32 of the block, code half g): 2 x 32
+// codes, loaded with coalesced 16-byte planes.
+//
+// Codes become bf16 pairs without float arithmetic: 0x4300 | q is the bf16
+// value 128 + q for q < 128, so a pair of codes (2i, 2i+1) in one dword meets
+// the raw bf16 activation pair (x[2i], x[2i+1]) in v_dot2_f32_bf16. Per unit,
+//   sum_k x_k (s q_k + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k.
+// 8-bit codes (up to 255) are converted exactly instead, with offset 0.
+// ---------------------------------------------------------------------------
+typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
+typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                         __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+template <int BITS, int MT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
+    const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
+    int gs_log2, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  __shared__ float part[WPB][64][MT];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, g2 = lane >> 5;
+  const int rb = blockIdx.x;
+  const int m0 = blockIdx.y * MT;
+  const int mcount = min(MT, M - m0);
+  const int nk = K / 64;
+  const int gp = gs_log2 == 5 ? 2 : 1;
+  const int rs = 512 * BITS + 256 * gp;
+  const __amdgpu_buffer_rsrc_t wrs =
+      rsrc(tw + static_cast<int64_t>(rb) * nk * rs, static_cast<uint32_t>(nk) * rs);
+  int wvo[2], rvo[2], svo[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    wvo[nb] = nb * tiled::half_bytes(BITS) + lane * 16;
+    rvo[nb] = nb * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
+    svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * gp + (gp == 2 ? g2 : 0)) * 4;
+  }
+  // activations: this lane's 32-code half of each step
+  __amdgpu_buffer_rsrc_t xrs[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    xrs[m] = rsrc(x + static_cast<int64_t>(m0 + min(m, mcount - 1)) * K,
+                  static_cast<uint32_t>(K) * 2);
+  const int xvo = 32 * g2 * 2;
+
+  const int per = (nk + WPB - 1) / WPB;
+  const int k_begin = wave * per, k_end = min(nk, k_begin + per);
+
+  float acc[2][MT];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[nb][m] = 0.f;
+
+  for (int kk = k_begin; kk < k_end; ++kk) {
+    const int so = kk * rs;
+    uint32_t w[2][BITS];
+    uint32_t sb[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int p = 0; p < FP; ++p) {
+        const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+        w[nb][4 * p] = v.x; w[nb][4 * p + 1] = v.y; w[nb][4 * p + 2] = v.z; w[nb][4 * p + 3] = v.w;
+      }
+      if constexpr (RW == 1) {
+        w[nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+      } else if constexpr (RW == 2) {
+        const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
+        w[nb][4 * FP] = v.x; w[nb][4 * FP + 1] = v.y;
+      } else if constexpr (RW == 3) {
+        const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
+        w[nb][4 * FP] = v.x; w[nb][4 * FP + 1] = v.y; w[nb][4 * FP + 2] = v.z;
+      }
+      sb[nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+    }
+    float dq[2][MT], xs[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      xs[m] = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) dq[nb][m] = 0.f;
+    }
+    // 4 chunks of 8 codes: 4 code pairs per unit against 4 activation pairs
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t xv[MT][4];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const v4u_t v =
+            __builtin_amdgcn_raw_buffer_load_b128(xrs[m], xvo + c * 16, kk * 128, 0);
+        xv[m][0] = v.x; xv[m][1] = v.y; xv[m][2] = v.z; xv[m][3] = v.w;
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xs[m] = dot2_bf16(xv[m][j], 0x3F803F80u, xs[m]);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 8 * c + 2 * j;
+          uint32_t pr;
+          if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
+            pr = pack_bf16x2(static_cast<float>(code_at<BITS>(w[nb], i)),
+                             static_cast<float>(code_at<BITS>(w[nb], i + 1)));
+          else
+            pr = (code_at<BITS>(w[nb], i) | (code_at<BITS>(w[nb], i + 1) << 16)) | 0x43004300u;
+#pragma unroll
+          for (int m = 0; m < MT; ++m) dq[nb][m] = dot2_bf16(pr, xv[m][j], dq[nb][m]);
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float sc = __uint_as_float(sb[nb] << 16);
+      const float bi = __uint_as_float(sb[nb] & 0xFFFF0000u);
+      const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[nb][m] = fmaf(sc, dq[nb][m], fmaf(b2, xs[m], acc[nb][m]));
+    }
+  }
+
+  // the two code halves of each row meet across lanes l and l+32
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[nb][m] += __shfl_xor(acc[nb][m], 32, 64);
+  if (g2 == 0) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) part[wave][nb * 32 + l32][m] = acc[nb][m];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int n = rb * 64 + lane;
+  if (n >= N) return;
+  const float bv = bias ? bf16_to_f32(bias[n]) : 0.f;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m >= mcount) break;
+    float t = bv;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) t += part[w][lane][m];
+    y[static_cast<int64_t>(m0 + m) * N + n] = f32_to_bf16(t);
+  }
+}
+
+template <int BITS, int MT>
+hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
+                         const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  const int gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
+  constexpr int WPB = 8;
+  dim3 grid((N + 63) / 64, (M + MT - 1) / MT);
+  qmv_tiled_kernel<BITS, MT, WPB><<<grid, 64 * WPB, 0, s>>>(
+      x, M, K, static_cast<const uint8_t*>(tw), N, gs_log2, bias, y);
+  return hipGetLastError();
+}
+
+template <int BITS>
+hipError_t pick_mt_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
+                         const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M <= 1) return run_qmv_tiled<BITS, 1>(x, M, K, tw, N, gs, bias, y, s);
+  if (M <= 2) return run_qmv_tiled<BITS, 2>(x, M, K, tw, N, gs, bias, y, s);
+  if (M <= 4) return run_qmv_tiled<BITS, 4>(x, M, K, tw, N, gs, bias, y, s);
+  return run_qmv_tiled<BITS, 8>(x, M, K, tw, N, gs, bias, y, s);
+}
+
 }  // namespace
 
 namespace detail {
@@ -238,6 +421,20 @@ hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,
     case 5: return pick_mt<5>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 6: return pick_mt<6>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 8: return pick_mt<8>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
+                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  switch (bits) {
+    case 2: return pick_mt_tiled<2>(x, M, K, tw, N, gs, bias, y, s);
+    case 3: return pick_mt_tiled<3>(x, M, K, tw, N, gs, bias, y, s);
+    case 4: return pick_mt_tiled<4>(x, M, K, tw, N, gs, bias, y, s);
+    case 5: return pick_mt_tiled<5>(x, M, K, tw, N, gs, bias, y, s);
+    case 6: return pick_mt_tiled<6>(x, M, K, tw, N, gs, bias, y, s);
+    case 8: return pick_mt_tiled<8>(x, M, K, tw, N, gs, bias, y, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -14,6 +14,12 @@ load() infers bits = 32*wCols/in and groupSize = in/sCols, casts scales/biases
 to the compute dtype; forward() casts x to bf16, runs the quantized matmul,
 then adds the bias. Here the bias add is fused into the kernel epilogue (added
 in fp32 before the single bf16 rounding).
+
+Both keep the MLX triple as their parameters and, when the geometry allows
+(K % 64 == 0, bf16 scales/biases), also a tiled copy of the same bits built on
+first use; calls then run the tiled kernels, whose results are bit-identical
+to the MLX-layout kernels. The copy costs one more weight's worth of HBM
+(K*N*bits/8 + scale/bias bytes); `tiled=False` turns it off.
 """
 import math
 
@@ -24,9 +30,13 @@ from .weights import get_quantized, infer_geometry
 
 
 class QuantizedLinear:
+    tiled = True  # class default; from_weights / __init__ may override per instance
+    _tw = None
+
     def __init__(self, input_dims, output_dims, bias=True, group_size=64, bits=4,
-                 device="cuda", seed=None):
+                 device="cuda", seed=None, tiled=True):
         # MLXNN initialises uniform(-1/sqrt(in), 1/sqrt(in)) and quantizes it.
+        self.tiled = bool(tiled)
         self.input_dims = int(input_dims)
         self.output_dims = int(output_dims)
         self.group_size = int(group_size)
@@ -42,9 +52,11 @@ class QuantizedLinear:
                      if bias else None)
 
     @classmethod
-    def from_weights(cls, weight, scales, biases, bias=None, group_size=64, bits=4):
+    def from_weights(cls, weight, scales, biases, bias=None, group_size=64, bits=4,
+                     tiled=True):
         """Wrap an existing packed triple (as update(parameters:) does)."""
         obj = cls.__new__(cls)
+        obj.tiled = bool(tiled)
         obj.weight = weight
         obj.scales = scales
         obj.biases = biases
@@ -73,13 +85,26 @@ class QuantizedLinear:
             self.bias = parameters["bias"]
         self.output_dims = int(self.weight.shape[0])
         self.input_dims = int(self.weight.shape[1] * 32 // self.bits)
+        self._tw = None
         return self
 
     @property
     def shape(self):
         return (self.output_dims, self.input_dims)
 
+    def tiled_weight(self):
+        """The tiled copy of the weight, built on first use; None when the
+        geometry does not allow one or tiling is off."""
+        if self._tw is None and self.tiled and ops.tiled_supported(
+                self.input_dims, self.group_size, self.bits, self.scales.dtype):
+            self._tw = ops.tile(self.weight, self.scales, self.biases, self.group_size,
+                                self.bits)
+        return self._tw
+
     def __call__(self, x):
+        tw = self.tiled_weight()
+        if tw is not None and x.dtype == torch.bfloat16 and x.shape[-1] == tw.K:
+            return ops.tiled_matmul(x, tw, bias=self.bias)
         return ops.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                                     group_size=self.group_size, bits=self.bits, bias=self.bias)
 
@@ -99,6 +124,8 @@ class MfLinear:
         self.bias = None
         self.bits = 0
         self.group_size = 0
+        self.tiled = True
+        self._tw = None
 
     @classmethod
     def load(cls, weights, prefix, in_features, dtype=torch.bfloat16):
@@ -132,6 +159,12 @@ class MfLinear:
             if self.scales.dtype != torch.bfloat16:
                 raise ValueError("MfLinear: the quantized kernels take bfloat16 scales/biases")
             xc = x.to(torch.bfloat16).contiguous()
+            if self._tw is None and self.tiled and ops.tiled_supported(
+                    self.in_dim, self.group_size, self.bits, self.scales.dtype):
+                self._tw = ops.tile(self.w, self.scales, self.biases, self.group_size,
+                                    self.bits)
+            if self._tw is not None:
+                return ops.tiled_matmul(xc, self._tw, bias=self.bias)
             return ops.quantized_matmul(xc, self.w, self.scales, self.biases, transpose=True,
                                         group_size=self.group_size, bits=self.bits,
                                         bias=self.bias)

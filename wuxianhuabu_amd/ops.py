@@ -194,6 +194,86 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
     return y
 
 
+class TiledWeight:
+    """A packed weight reordered into the tiled load-time layout (uint8 device
+    buffer) plus its geometry. Built once by `tile()`; read by `tiled_matmul`.
+    Holds the same bits as the MLX triple, so results are identical."""
+
+    __slots__ = ("data", "N", "K", "group_size", "bits")
+
+    def __init__(self, data, N, K, group_size, bits):
+        self.data, self.N, self.K = data, int(N), int(K)
+        self.group_size, self.bits = int(group_size), int(bits)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def nbytes(self):
+        return self.data.numel()
+
+
+def tiled_supported(K, group_size, bits, scales_dtype=torch.bfloat16):
+    """Whether `tile()` accepts this geometry (K % 64 == 0, bf16 scales)."""
+    return (K > 0 and K % 64 == 0 and K % group_size == 0 and bits in _SUPPORTED_BITS and
+            group_size in _SUPPORTED_GS and scales_dtype == torch.bfloat16)
+
+
+def tile(w, scales, biases, group_size=64, bits=4):
+    """MLX-layout triple -> TiledWeight (one device pass, no requantization)."""
+    _check_bits_gs("tile", bits, group_size)
+    w = _as_words(w)
+    _on_gpu("tile", w, scales, biases)
+    if w.ndim != 2:
+        raise ValueError(f"[tile] The weight matrix must be 2-D (got {w.ndim}-D).")
+    N, K = int(w.shape[0]), int(w.shape[1]) * 32 // bits
+    if w.shape[1] * 32 % bits != 0 or tuple(scales.shape) != (N, K // group_size) or \
+            scales.shape != biases.shape:
+        raise ValueError(f"[tile] Shape of scales and biases does not match the matrix given "
+                         f"the quantization parameters (w {tuple(w.shape)}, scales "
+                         f"{tuple(scales.shape)}, group_size={group_size}, bits={bits}).")
+    if scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        raise ValueError("[tile] scales and biases must be bfloat16.")
+    L = _lib.lib()
+    nbytes = L.mxq_tiled_bytes(N, K, group_size, bits)
+    if nbytes < 0:
+        _lib.check(int(nbytes))
+    w, scales, biases = _dense(w), _dense(scales), _dense(biases)
+    data = torch.empty(int(nbytes), dtype=torch.uint8, device=w.device)
+    _lib.check(L.mxq_tile(_ptr(w), _ptr(scales), _ptr(biases), N, K, group_size, bits,
+                          _ptr(data), _stream(w)))
+    return TiledWeight(data, N, K, group_size, bits)
+
+
+def tiled_matmul(x, tw, *, bias=None, path="auto"):
+    """quantized_matmul(x, w, scales, biases, transpose=True, ...) on a TiledWeight.
+
+    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv"."""
+    op = "quantized_matmul"
+    if not isinstance(tw, TiledWeight):
+        raise ValueError(f"[{op}] expected a TiledWeight (got {type(tw).__name__}).")
+    _on_gpu(op, x, tw.data, bias)
+    if x.shape[-1] != tw.K:
+        raise ValueError(f"[{op}] x.shape[-1] == {x.shape[-1]} does not match the weight's "
+                         f"input dimension {tw.K}.")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"[{op}] x must be bfloat16 (got {x.dtype}).")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (tw.N,)):
+        raise ValueError(f"[{op}] bias must be bfloat16 of shape ({tw.N},).")
+    x, bias = _dense(x), _dense(bias)
+    M = x.numel() // tw.K
+    y = torch.empty(tuple(x.shape[:-1]) + (tw.N,), dtype=torch.bfloat16, device=x.device)
+    fns = {"auto": "mxq_quantized_matmul_tiled", "qmm": "mxq_qmm_tiled",
+           "qmv": "mxq_qmv_tiled"}
+    if path not in fns:
+        raise ValueError(f"unknown path {path!r}")
+    fn = getattr(_lib.lib(), fns[path])
+    _lib.check(fn(_ptr(x), M, tw.K, _ptr(tw.data), tw.N, tw.group_size, tw.bits, _ptr(bias),
+                  _ptr(y), _stream(x)))
+    return y
+
+
 # camelCase aliases, as the Swift surface spells them
 quantizedMatmul = quantized_matmul
 quantizedMM = quantized_matmul
