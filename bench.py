@@ -179,6 +179,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip oracle check and CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--all", action="store_true", help="also time c0, c1, c3-down, c4 chain")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run a plain elementwise copy of 1 GiB -> 1 GiB three times "
+                         "(the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -194,6 +197,13 @@ def main():
     torch.cuda.set_device(dev)
     steps, warmup = args.steps, args.warmup
     res = {}
+    if args.calibrate:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---------------- qmm (headline) ----------------
     c = QMM

@@ -28,7 +28,7 @@
 
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
-#include "mxq_tiled.hpp"
+#include "mxq_ring.hpp"
 
 namespace mxq {
 namespace {
@@ -37,6 +37,7 @@ constexpr int kBN = 256;       // output features per workgroup
 constexpr int kKS = 64;        // K step
 constexpr int kXPitch = 72;    // LDS row pitch in bf16 (64 + 8 padding)
 constexpr int kThreads = 256;
+constexpr int kGroupM = 4;     // token tiles swept together per XCD
 
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -74,11 +75,10 @@ __device__ __forceinline__ void buf_load_words(__amdgpu_buffer_rsrc_t r, int vof
   }
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  // word 3 = 0x00020000: raw (untyped) dword access on gfx9-family parts
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
-                                           0x00020000);
-}
+using ring::make_rsrc;
+using ring::ring_barrier;
+using ring::swz;
+using ring::wait_vmcnt;
 
 // 32 codes -> four MFMA operands of 8 bf16 (w = q*s + b, fp32 then RNE).
 template <int BITS>
@@ -121,19 +121,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
 
-  // ---- tile order: XCD-contiguous ranges, then groups of 8 token tiles ----
-  const int tiles = m_tiles * n_tiles;
-  int bid = blockIdx.x;
-  const int nblk = gridDim.x;  // padded to a multiple of 8 by the launcher
-  bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  if (bid >= tiles) return;
-  constexpr int GROUP_M = 8;
-  const int per_group = GROUP_M * n_tiles;
-  const int first_m = (bid / per_group) * GROUP_M;
-  const int gsize = min(m_tiles - first_m, GROUP_M);
-  const int in_group = bid % per_group;
-  const int m_tile = first_m + in_group % gsize;
-  const int n_tile = in_group / gsize;
+  int m_tile, n_tile;
+  if (!ring::tile_coords<kGroupM>(m_tiles, n_tiles, m_tile, n_tile)) return;
   const int m0 = m_tile * BM, n0 = n_tile * kBN;
 
   const int WB = K / 32 * BITS * 4;  // packed row bytes
@@ -329,53 +318,22 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
 constexpr int kXStages = 4;
 constexpr int kWSlots = 4;
 
-__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-// 16 bytes per lane from the buffer straight into LDS at dst + 16*lane
-// (buffer_load_dwordx4 ... lds; dst must be wave-uniform).
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* dst, int voff,
-                                           int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
-}
-
-// vmcnt-only wait (expcnt and lgkmcnt left at their maxima) for gfx9 encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier for the ring: this wave's LDS-direct loads for the next
-// stage have landed (vmcnt(N), later requests stay in flight) and its LDS
-// reads are done (lgkmcnt(0)), then s_barrier. __syncthreads() would also wait
-// for every outstanding global load (vmcnt(0)), emptying the prefetch ring.
-template <int N>
-__device__ __forceinline__ void ring_barrier() {
-  wait_vmcnt<N>();
-  __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 template <int BITS>
 struct RunLoads {  // VMEM instructions per 32-code run load
   static constexpr int value = BITS == 5 || BITS == 6 || BITS == 8 ? 2 : 1;
 };
 
-template <int BITS, int BM, bool TILED>
+template <int BITS, int BM>
 __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint8_t* __restrict__ tw, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ y, int M, int N, int K, int gs_log2, int m_tiles, int n_tiles) {
   constexpr int MB = BM / 32;            // 32-token blocks per wave
   constexpr int XL = BM / 32;            // LDS-direct loads per wave per K step (8 rows each)
   constexpr int STAGE = BM * 64;         // bf16 elements per LDS stage
-  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
   // weight VMEM instructions per K step per lane
-  constexpr int WLOADS = TILED ? 2 * (FP + (RW > 0 ? 1 : 0) + 1) : 2 * (RunLoads<BITS>::value + 2);
+  constexpr int WLOADS = 2 * (RunLoads<BITS>::value + 2);
   constexpr int LOADS_PER_STEP = WLOADS + XL;
   __shared__ __attribute__((aligned(16))) uint16_t xs[kXStages * STAGE];
 
@@ -384,19 +342,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
 
-  // ---- tile order: XCD-contiguous ranges, then groups of 8 token tiles ----
-  const int tiles = m_tiles * n_tiles;
-  int bid = blockIdx.x;
-  const int nblk = gridDim.x;  // padded to a multiple of 8 by the launcher
-  bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  if (bid >= tiles) return;
-  constexpr int GROUP_M = 8;
-  const int per_group = GROUP_M * n_tiles;
-  const int first_m = (bid / per_group) * GROUP_M;
-  const int gsize = min(m_tiles - first_m, GROUP_M);
-  const int in_group = bid % per_group;
-  const int m_tile = first_m + in_group % gsize;
-  const int n_tile = in_group / gsize;
+  int m_tile, n_tile;
+  if (!ring::tile_coords<kGroupM>(m_tiles, n_tiles, m_tile, n_tile)) return;
   const int m0 = m_tile * BM, n0 = n_tile * kBN;
 
   const int WB = K / 32 * BITS * 4;  // packed row bytes
@@ -406,24 +353,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
 
   const __amdgpu_buffer_rsrc_t xrs =
       make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(rows_m) * K * 2);
-  // weights: MLX rows of this tile, or the tiled records of this wave's
-  // 64-row block (all offsets per lane fixed; the K step is a scalar offset)
-  const int gp = gs_log2 == 5 ? 2 : 1;
-  const int rs = TILED ? 512 * BITS + 256 * gp : 0;  // tiled record bytes
+  // weights: the MLX rows of this tile (all offsets per lane fixed; the K
+  // step is a scalar offset)
   __amdgpu_buffer_rsrc_t wrs, srs, brs;
-  int wvo[2], rvo[2], svo[2];
-  if constexpr (TILED) {
-    const int rb = min((n0 >> 6) + wave, (N + 63) / 64 - 1);
-    wrs = make_rsrc(tw + static_cast<int64_t>(rb) * nk * rs, static_cast<uint32_t>(nk) * rs);
-    srs = wrs;
-    brs = wrs;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      wvo[nb] = nb * tiled::half_bytes(BITS) + lane * 16;
-      rvo[nb] = nb * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
-      svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * gp + (gp == 2 ? g2 : 0)) * 4;
-    }
-  } else {
+  int wvo[2], svo[2];
+  {
     wrs = make_rsrc(reinterpret_cast<const char*>(wq) + static_cast<int64_t>(n0) * WB,
                     static_cast<uint32_t>(rows_n) * WB);
     srs = make_rsrc(scales + static_cast<int64_t>(n0) * G, static_cast<uint32_t>(rows_n) * G * 2);
@@ -432,7 +366,6 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
     for (int nb = 0; nb < 2; ++nb) {
       const int r = min(wave * 64 + nb * 32 + l32, rows_n - 1);
       wvo[nb] = r * WB + g2 * BITS * 4;
-      rvo[nb] = 0;
       svo[nb] = r * G * 2 + ((32 * g2) >> gs_log2) * 2;
     }
   }
@@ -456,51 +389,36 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x16{};
 
+  // The issue order of every load is pinned (sched_barrier after each): the
+  // compiler derives its vmcnt waits from program order, and a prologue whose
+  // loads were reordered relative to the loop body would make those waits, which
+  // are the minimum over both paths, far stricter than the ring needs.
   auto load_w = [&](int kk, RawW<BITS>& r) {
-    if constexpr (TILED) {
-      const int so = kk * rs;
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int p = 0; p < FP; ++p) {
-          const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
-          r.w[nb][4 * p] = v.x; r.w[nb][4 * p + 1] = v.y;
-          r.w[nb][4 * p + 2] = v.z; r.w[nb][4 * p + 3] = v.w;
-        }
-        if constexpr (RW == 1) {
-          r.w[nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
-        } else if constexpr (RW == 2) {
-          const v2u v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
-          r.w[nb][4 * FP] = v.x; r.w[nb][4 * FP + 1] = v.y;
-        } else if constexpr (RW == 3) {
-          const v3u v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
-          r.w[nb][4 * FP] = v.x; r.w[nb][4 * FP + 1] = v.y; r.w[nb][4 * FP + 2] = v.z;
-        }
-        r.s[nb] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], so, 0);
-        r.b[nb] = 0u;
-      }
-    } else {
+    {
       const int so = kk * (8 * BITS);
       const int ss = ((kk * kKS) >> gs_log2) * 2;
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         buf_load_words<BITS>(wrs, wvo[nb], so, r.w[nb]);
+        __builtin_amdgcn_sched_barrier(0);
         r.s[nb] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
+        __builtin_amdgcn_sched_barrier(0);
         r.b[nb] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
-  // scale and bias of row block nb from the raw bits (tiled: one dword, scale
-  // in the low half; MLX: two bf16 loads)
+  // scale and bias of row block nb from the raw bf16 bits
   auto scale_bias = [&](const RawW<BITS>& r, int nb, float& sc, float& bi) {
     sc = __uint_as_float(r.s[nb] << 16);
-    bi = TILED ? __uint_as_float(r.s[nb] & 0xFFFF0000u) : __uint_as_float(r.b[nb] << 16);
+    bi = __uint_as_float(r.b[nb] << 16);
   };
   auto load_x = [&](int kk, int stage) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       uint16_t* dst = xs + stage * STAGE + (wave * XL + i) * 512;
-      lds_load16(xrs, dst, xvo[i], kk * kKS * 2);
+      ring::lds_load<16>(xrs, dst, xvo[i], kk * kKS * 2);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   auto read_frags = [&](int stage, int mb, bf16x8 (&f)[4]) {
@@ -510,91 +428,106 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_ring_kernel(
   };
 
   RawW<BITS> rw[kWSlots];
+#pragma unroll
+  for (int i = 0; i < kWSlots; ++i) rw[i] = RawW<BITS>{};
   uint32_t wu[2][2][16];  // unpacked bf16 pairs: [buffer][row block][dword]
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) wu[i][j][k] = 0u;
+  // the pipeline's third fill step multiplies stage 2 by wu[0]: both start at
+  // exact zeros, so that step adds +0 to every accumulator whatever the inputs
+  {
+    u32x4a* st2 = reinterpret_cast<u32x4a*>(xs + 2 * STAGE);
+#pragma unroll
+    for (int i = tid; i < STAGE / 8; i += kThreads) st2[i] = u32x4a{0u, 0u, 0u, 0u};
+  }
 
-  // One K step. J = kk mod 4 picks the register/LDS slots at compile time.
+  // unpack dwords [d0, d1) of raw slot r into wu buffer b
+  // (the bounds are constants once the callers' loops are unrolled)
+  auto unpack = [&](const RawW<BITS>& r, uint32_t (&dst)[2][16], float s0, float b0, float s1,
+                    float b1, int d0, int d1) {
+#pragma unroll
+    for (int d = d0; d < d1; ++d) {
+      const int nb = d / 16, i = d % 16;
+      const float sc = nb ? s1 : s0, bi = nb ? b1 : b0;
+      dst[nb][i] = pack_bf16x2(fmaf(static_cast<float>(code_at<BITS>(r.w[nb], 2 * i)), sc, bi),
+                               fmaf(static_cast<float>(code_at<BITS>(r.w[nb], 2 * i + 1)), sc, bi));
+    }
+  };
+
+  // One K step. J = (kk + 3) mod 4 picks the register/LDS slots at compile
+  // time. Step kk requests step kk+3's weights and activations, unpacks step
+  // kk+1's weights (requested two steps earlier) and multiplies step kk's.
   // Source order is the schedule (sched_barrier fences keep it): per 32-token
-  // block, the next block's LDS reads, then four pairs of MFMAs each followed
-  // by one 2-code slice of the next step's unpacking.
+  // block, the next block's LDS reads, then four pairs of MFMAs each followed by
+  // one 2-code slice of the unpacking. The pipeline fill (kk = -3, -2, -1) runs
+  // this same code, so the compiler's vmcnt waits and the ring barrier's count
+  // follow one fixed issue order: steps -3 and -2 only request; step -1 also
+  // unpacks step 0 and multiplies the zeroed stage 2 by the zeroed wu[0].
   auto step = [&](auto Jc, int kk) {
     constexpr int J = decltype(Jc)::value;
     constexpr int XS = J % kXStages;        // stage holding step kk
     constexpr int F = J % 2, FN = (J + 1) % 2;
     const RawW<BITS>& nr = rw[(J + 1) % kWSlots];
-    // requests for step kk+3 (clamped; a repeated request is harmless)
+    // requests for step kk+3 (clamped at the end: a repeated request is
+    // harmless and keeps every step's request count equal)
     const int kl = min(kk + 3, nk - 1);
     load_w(kl, rw[(J + 3) % kWSlots]);
     load_x(kl, (J + 3) % kXStages);
     float s0, b0, s1, b1;
     scale_bias(nr, 0, s0, b0);
     scale_bias(nr, 1, s1, b1);
-    // steps past K (the loop runs a multiple of 4 steps) only keep the
-    // request/barrier cadence
-    if (kk < nk) {
-    bf16x8 xa[4], xb[4];
-    read_frags(XS, 0, xa);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      bf16x8 (&cur)[4] = (mb & 1) ? xb : xa;
-      bf16x8 (&nxt)[4] = (mb & 1) ? xa : xb;
-      if (mb + 1 < MB) read_frags(XS, mb + 1, nxt);
+    if (kk >= -1) {
+      bf16x8 xa[4], xb[4];
+      read_frags(XS, 0, xa);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const bf16x8 wv = __builtin_bit_cast(
-              bf16x8, v4u{wu[F][nb][4 * sl], wu[F][nb][4 * sl + 1], wu[F][nb][4 * sl + 2],
-                          wu[F][nb][4 * sl + 3]});
-          acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, cur[sl], acc[nb][mb], 0, 0, 0);
-        }
-        // slices: (MB * 4) slots cover the 32 dwords of the next step's operands
-        constexpr int SLOTS = MB * 4;
-#pragma unroll
-        for (int d = (mb * 4 + sl) * 32 / SLOTS; d < (mb * 4 + sl + 1) * 32 / SLOTS; ++d) {
-          const int nb = d / 16, i = d % 16;
-          const float sc = nb ? s1 : s0, bi = nb ? b1 : b0;
-          wu[FN][nb][i] = pack_bf16x2(
-              fmaf(static_cast<float>(code_at<BITS>(nr.w[nb], 2 * i)), sc, bi),
-              fmaf(static_cast<float>(code_at<BITS>(nr.w[nb], 2 * i + 1)), sc, bi));
-        }
+      for (int mb = 0; mb < MB; ++mb) {
+        bf16x8 (&cur)[4] = (mb & 1) ? xb : xa;
+        bf16x8 (&nxt)[4] = (mb & 1) ? xa : xb;
+        if (mb + 1 < MB) read_frags(XS, mb + 1, nxt);
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const bf16x8 wv = __builtin_bit_cast(
+                bf16x8, v4u{wu[F][nb][4 * sl], wu[F][nb][4 * sl + 1], wu[F][nb][4 * sl + 2],
+                            wu[F][nb][4 * sl + 3]});
+            acc[nb][mb] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, cur[sl], acc[nb][mb], 0, 0, 0);
+          }
+          // slices: (MB * 4) slots cover the 32 dwords of the next step's operands
+          constexpr int SLOTS = MB * 4;
+          unpack(nr, wu[FN], s0, b0, s1, b1, (mb * 4 + sl) * 32 / SLOTS,
+                 (mb * 4 + sl + 1) * 32 / SLOTS);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
-    }
-    // the stage of step kk+1 was requested two steps ago: wait for this wave's
-    // part of it (everything issued later may stay in flight), then publish
+    // step kk+1's stage was requested in step kk-2: wait for this wave's part
+    // of it (the requests of steps kk-1 and kk may stay in flight), then publish
     ring_barrier<2 * LOADS_PER_STEP>();
   };
 
-  // ---- prologue: steps 0..2 requested, step 0 unpacked ----
-  load_w(0, rw[0]);
-  load_x(0, 0);
-  load_w(min(1, nk - 1), rw[1]);
-  load_x(min(1, nk - 1), 1);
-  load_w(min(2, nk - 1), rw[2]);
-  load_x(min(2, nk - 1), 2);
-  {
-    float s0, b0, s1, b1;
-    scale_bias(rw[0], 0, s0, b0);
-    scale_bias(rw[0], 1, s1, b1);
-#pragma unroll
-    for (int d = 0; d < 32; ++d) {
-      const int nb = d / 16, i = d % 16;
-      const float sc = nb ? s1 : s0, bi = nb ? b1 : b0;
-      wu[0][nb][i] = pack_bf16x2(fmaf(static_cast<float>(code_at<BITS>(rw[0].w[nb], 2 * i)), sc, bi),
-                                 fmaf(static_cast<float>(code_at<BITS>(rw[0].w[nb], 2 * i + 1)), sc, bi));
-    }
-  }
-  ring_barrier<2 * LOADS_PER_STEP>();
-
-  for (int kk = 0; kk < nk; kk += 4) {
+  // stage 2 zeroed by every wave before anyone multiplies it
+  ring_barrier<0>();
+  for (int kk = -3;;) {
     step(std::integral_constant<int, 0>{}, kk);
-    step(std::integral_constant<int, 1>{}, kk + 1);
-    step(std::integral_constant<int, 2>{}, kk + 2);
-    step(std::integral_constant<int, 3>{}, kk + 3);
+    if (++kk >= nk) break;
+    step(std::integral_constant<int, 1>{}, kk);
+    if (++kk >= nk) break;
+    step(std::integral_constant<int, 2>{}, kk);
+    if (++kk >= nk) break;
+    step(std::integral_constant<int, 3>{}, kk);
+    if (++kk >= nk) break;
   }
+  // no LDS-direct load may still be in flight when the workgroup's LDS is
+  // released (the last steps' requests repeat step nk-1 and are never read)
+  wait_vmcnt<0>();
 
   // ---- epilogue: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3) for one token m ----
 #pragma unroll
@@ -637,19 +570,18 @@ inline Grid grid_for(int M, int N, int BM, int gs) {
   Grid g;
   g.m_tiles = (M + BM - 1) / BM;
   g.n_tiles = (N + kBN - 1) / kBN;
-  g.blocks = (g.m_tiles * g.n_tiles + 7) / 8 * 8;  // whole XCD rounds
+  g.blocks = ring::grid_blocks(g.m_tiles * g.n_tiles);
   g.gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
   return g;
 }
 
-template <int BITS, int BM, bool TILED>
+template <int BITS, int BM>
 hipError_t run_ring(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
-                    const uint16_t* bi, const void* tw, int N, int gs, const uint16_t* bias,
-                    uint16_t* y, hipStream_t s) {
+                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                    hipStream_t s) {
   const Grid g = grid_for(M, N, BM, gs);
-  qmm_ring_kernel<BITS, BM, TILED><<<g.blocks, kThreads, 0, s>>>(
-      x, wq, sc, bi, static_cast<const uint8_t*>(tw), bias, y, M, N, K, g.gs_log2, g.m_tiles,
-      g.n_tiles);
+  qmm_ring_kernel<BITS, BM><<<g.blocks, kThreads, 0, s>>>(x, wq, sc, bi, bias, y, M, N, K,
+                                                          g.gs_log2, g.m_tiles, g.n_tiles);
   return hipGetLastError();
 }
 
@@ -675,8 +607,8 @@ hipError_t pick_bm(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
                    const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
                    hipStream_t s) {
   if (K % kKS == 0 && M > 64) {
-    if (M <= 128) return run_ring<BITS, 128, false>(x, M, K, wq, sc, bi, nullptr, N, gs, bias, y, s);
-    return run_ring<BITS, 256, false>(x, M, K, wq, sc, bi, nullptr, N, gs, bias, y, s);
+    if (M <= 128) return run_ring<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+    return run_ring<BITS, 256>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
   }
   if (M <= 64) return run_step<BITS, 64>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
   return run_step<BITS, 128>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
@@ -688,28 +620,6 @@ namespace detail {
 
 bool qmm_supports_bits(int bits) {
   return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
-}
-
-template <int BITS>
-hipError_t pick_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
-                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  if (M <= 128)
-    return run_ring<BITS, 128, true>(x, M, K, nullptr, nullptr, nullptr, tw, N, gs, bias, y, s);
-  return run_ring<BITS, 256, true>(x, M, K, nullptr, nullptr, nullptr, tw, N, gs, bias, y, s);
-}
-
-hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
-                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  if (M == 0 || N == 0) return hipSuccess;
-  switch (bits) {
-    case 2: return pick_tiled<2>(x, M, K, tw, N, gs, bias, y, s);
-    case 3: return pick_tiled<3>(x, M, K, tw, N, gs, bias, y, s);
-    case 4: return pick_tiled<4>(x, M, K, tw, N, gs, bias, y, s);
-    case 5: return pick_tiled<5>(x, M, K, tw, N, gs, bias, y, s);
-    case 6: return pick_tiled<6>(x, M, K, tw, N, gs, bias, y, s);
-    case 8: return pick_tiled<8>(x, M, K, tw, N, gs, bias, y, s);
-    default: return hipErrorInvalidValue;
-  }
 }
 
 hipError_t launch_qmm(const uint16_t* x, int M, int K, const uint32_t* wq,
