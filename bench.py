@@ -88,14 +88,43 @@ def time_launches(torch, fn, steps, warmup, rotate=1):
     return per, total
 
 
+def time_graph(torch, fn, launches, replays, rotate=1):
+    """Per-launch duration (ms) of `launches` back-to-back launches captured in
+    one HIP graph (no host gaps between them), from HIP events around each of
+    `replays` replays on the launching stream. Returns (per-launch ms of each
+    replay, total ms)."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(rotate):  # warm the launch path outside the capture
+            fn(i)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(launches):
+                fn(i % rotate)
+        g.replay()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+        ev[0].record(s)
+        for i in range(replays):
+            g.replay()
+            ev[i + 1].record(s)
+        torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) / launches for i in range(replays)]
+    return per, ev[0].elapsed_time(ev[replays])
+
+
 def load_traffic(kernel_key):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
-    scaled by a copy-kernel calibration; committed under profiles/."""
+    """Memory-side bytes per launch of one kernel, measured with rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy
+    kernel of known size) and committed in profiles/traffic.json; None if absent."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kernel_key)
-    except (OSError, ValueError):
+            k = json.load(f)["kernels"].get(kernel_key)
+        return None if k is None else k["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
         return None
 
 
@@ -153,6 +182,21 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
         "sample": f"{nrows} of {qmm_c['M']} rows of the qmm workload (mlx CPU qmm loop "
                   f"restated in C, bf16 arithmetic), {t:.1f} s; the loop is linear in M",
     }
+    # the same loop over all host cores this process may use (OpenMP over N), on a
+    # sample sized to the same budget
+    nthr = threads
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=nthr)
+    t_row = time.perf_counter() - t0
+    nrows_mc = int(max(1, min(256, budget_s / 2 / max(t_row, 1e-3))))
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0,
+                  rows=np.arange(nrows_mc, dtype=np.int64), threads=nthr)
+    tmc = time.perf_counter() - t0
+    out["cpu_baseline_all_cores"] = {
+        "value": 2.0 * nrows_mc * N * K / tmc / 1e12, "unit": "TFLOP/s", "cores": nthr,
+        "kind": "port",
+        "sample": f"{nrows_mc} of {qmm_c['M']} rows, {tmc:.1f} s, OpenMP over N"}
     # GEMV on the CPU: the full M=2 workload, 1 core
     t0 = time.perf_counter()
     O.qmm_mlx_cpu(host_u16(gx), host_u32(gwq), host_u16(gs_), host_u16(gb), gemv_c["gs"],
@@ -270,12 +314,15 @@ def main():
         ok(L.mxq_qmv(P(gx), g["M"], g["K"], P(wq_i), P(s_i), P(b_i), g["N"], g["gs"], g["bits"],
                      None, P(gy), cur()))
 
-    gsteps = max(steps * 10, 100)
-    mper, _ = time_launches(torch, gemv_mlx_launch, gsteps, warmup * 10, rotate=g["copies"])
+    # 100 launches per graph (20 passes over the 5 copies), replayed `steps` times
+    glaunch = 20 * g["copies"]
+    greplays = max(steps, 5)
+    mper, _ = time_graph(torch, gemv_mlx_launch, glaunch, greplays, rotate=g["copies"])
     mavg = sum(mper) / len(mper)
     res["gemv_mlx_layout"] = {"us_per_launch": mavg * 1e3,
                               "gbs": gemv_bytes(g) / (mavg * 1e-3) / 1e9}
-    gper, gtotal = time_launches(torch, gemv_launch, gsteps, warmup * 10, rotate=g["copies"])
+    gper, gtotal = time_graph(torch, gemv_launch, glaunch, greplays, rotate=g["copies"])
+    gsteps = glaunch * greplays
     gbytes = gemv_bytes(g)
     gavg = sum(gper) / len(gper)
     gemv_gbs = gbytes / (gavg * 1e-3) / 1e9
@@ -284,11 +331,12 @@ def main():
     res["gemv"] = {
         "metric": "GEMV GB/s at M=2", "value": gemv_bytes(g) / (gtotal / gsteps * 1e-3) / 1e9,
         "unit": "GB/s", "us_per_launch": gavg * 1e3, "launches": gsteps,
+        "timing": "HIP graph of 100 back-to-back launches, events around each replay",
         "config": {"workload": g["name"], "weight_copies_rotated": g["copies"],
                    "bytes_per_launch": gbytes},
         "roofline": {"bound": "hbm", "achieved": gemv_gbs, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": gemv_gbs / HBM_PEAK_GBS,
-                     "traffic": load_traffic("qmv_c2")},
+                     "traffic": load_traffic("qmv_tiled 6-bit M=2 K=4096 N=24576")},
     }
 
     # ---------------- optional extra configs ----------------
@@ -343,7 +391,7 @@ def main():
                    "weights": "resident, tiled at load (mxq_tile)", "tile_ms": tile_ms},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
-                     "traffic": load_traffic("qmm_c3_up"),
+                     "traffic": load_traffic("qmm_tiled 6-bit M=14400 K=4096 N=16384"),
                      "kernel_avg_ms": avg_ms, "kernel_median_ms": med_ms},
     }
     line.update(res)
