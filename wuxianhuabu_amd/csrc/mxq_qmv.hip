@@ -17,6 +17,7 @@
 // so each weight costs one decode and MT fused multiply-adds.
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
+#include "mxq_ring.hpp"
 #include "mxq_tiled.hpp"
 
 namespace mxq {
@@ -225,11 +226,20 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 }
 
 // ---------------------------------------------------------------------------
-// GEMV on the tiled layout (mxq_tiled.hpp). One workgroup per 64-row block;
-// its WPB waves split the block's K steps into contiguous ranges (the block's
-// records are contiguous in HBM, so each wave streams one span). Per step a
-// lane owns two units (rows r and r+32 of the block, code half g): 2 x 32
-// codes, loaded with coalesced 16-byte planes.
+// GEMV on the tiled layout (mxq_tiled.hpp). HBM-bound, so the design goal is
+// bytes in flight: one workgroup of 16 waves per 64-row block; the waves split
+// the block's K steps into contiguous spans (the block's records are
+// contiguous in HBM). Each wave, per batch of up to SPW steps:
+//   1. moves its activation slice (MT rows x SPW steps x 128 B) into its own
+//      LDS region with LDS-direct loads (no other wave reads it: no barrier);
+//   2. issues every weight load of the batch at once (SPW records of 64 rows x
+//      64 codes: 13 KB per wave at 6-bit, several hundred KB per CU);
+//   3. waits for the batch, sums each activation half-run once (32 codes of a
+//      row per lane half; the sums are shared by the 32 lanes of the half), and
+//      consumes the records. Sixteen waves per workgroup overlap one another's
+//      loads and arithmetic.
+// Per step a lane owns two units (rows r and r+32 of the block, code half g):
+// 2 x 32 codes from coalesced 16-byte planes.
 //
 // Codes become bf16 pairs without float arithmetic: 0x4300 | q is the bf16
 // value 128 + q for q < 128, so a pair of codes (2i, 2i+1) in one dword meets
@@ -241,47 +251,51 @@ typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 
+constexpr int kTiledWaves = 16;  // waves per workgroup (one 64-row block)
+constexpr int kTiledSPW = 4;     // steps per wave per batch
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                          __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
-                                           0x00020000);
-}
-
-template <int BITS, int MT, int WPB>
-__global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
+template <int BITS, int MT, int GP>
+__global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
-    int gs_log2, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+  constexpr int WPB = kTiledWaves, SPW = kTiledSPW;
   constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
-  __shared__ float part[WPB][64][MT];
+  constexpr int RB = tiled::code_bytes(BITS) + 256 * GP;      // record bytes
+  // activation bytes per wave, a whole number of LDS-direct loads (64 lanes x
+  // 16 B each): the padding of MT = 1 receives repeats of a valid row
+  constexpr int XW = (MT * SPW * 128 + 1023) / 1024 * 1024;
+  constexpr int XLOADS = XW / 1024;                           // LDS-direct loads per batch
+  constexpr int NSUM = MT * SPW * 2;                          // half-run sums per batch
+  static_assert(64 * MT * 4 <= XW, "partials reuse the activation region");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[WPB * XW];
+  __shared__ float xsum_all[WPB][NSUM];
+
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
   const int rb = blockIdx.x;
   const int m0 = blockIdx.y * MT;
   const int mcount = min(MT, M - m0);
-  const int nk = K / 64;
-  const int gp = gs_log2 == 5 ? 2 : 1;
-  const int rs = 512 * BITS + 256 * gp;
-  const __amdgpu_buffer_rsrc_t wrs =
-      rsrc(tw + static_cast<int64_t>(rb) * nk * rs, static_cast<uint32_t>(nk) * rs);
+  const int nk = K >> 6;
+  uint8_t* const xw = lds + wave * XW;
+  float* const xsum = xsum_all[wave];
+
+  const __amdgpu_buffer_rsrc_t wrs = ring::make_rsrc(
+      tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
+  const __amdgpu_buffer_rsrc_t xrs = ring::make_rsrc(
+      x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(mcount) * K * 2);
   int wvo[2], rvo[2], svo[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     wvo[nb] = nb * tiled::half_bytes(BITS) + lane * 16;
     rvo[nb] = nb * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
-    svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * gp + (gp == 2 ? g2 : 0)) * 4;
+    svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4;
   }
-  // activations: this lane's 32-code half of each step
-  __amdgpu_buffer_rsrc_t xrs[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-    xrs[m] = rsrc(x + static_cast<int64_t>(m0 + min(m, mcount - 1)) * K,
-                  static_cast<uint32_t>(K) * 2);
-  const int xvo = 32 * g2 * 2;
 
   const int per = (nk + WPB - 1) / WPB;
   const int k_begin = wave * per, k_end = min(nk, k_begin + per);
@@ -292,84 +306,126 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[nb][m] = 0.f;
 
-  for (int kk = k_begin; kk < k_end; ++kk) {
-    const int so = kk * rs;
-    uint32_t w[2][BITS];
-    uint32_t sb[2];
+  for (int b0 = k_begin; b0 < k_end; b0 += SPW) {
+    // 1. activations of steps b0 .. b0+SPW-1 (clamped; rows past M repeat a
+    //    valid row, their sums are never stored): LDS byte o of this wave's
+    //    region holds row o / (SPW*128), step (o / 128) % SPW, 16-byte chunk
+    //    (o / 16) % 8
+    __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-      for (int p = 0; p < FP; ++p) {
-        const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
-        w[nb][4 * p] = v.x; w[nb][4 * p + 1] = v.y; w[nb][4 * p + 2] = v.z; w[nb][4 * p + 3] = v.w;
-      }
-      if constexpr (RW == 1) {
-        w[nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
-      } else if constexpr (RW == 2) {
-        const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
-        w[nb][4 * FP] = v.x; w[nb][4 * FP + 1] = v.y;
-      } else if constexpr (RW == 3) {
-        const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
-        w[nb][4 * FP] = v.x; w[nb][4 * FP + 1] = v.y; w[nb][4 * FP + 2] = v.z;
-      }
-      sb[nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+    for (int i = 0; i < XLOADS; ++i) {
+      const int o = i * 1024 + lane * 16;
+      const int m = min(o / (SPW * 128), mcount - 1);
+      const int st = min(b0 + (o / 128) % SPW, k_end - 1);
+      ring::lds_load<16>(xrs, xw + i * 1024, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0);
     }
-    float dq[2][MT], xs[MT];
+    asm volatile("" ::: "memory");  // the activation request stays ahead of the wait below
+    // 2. every weight record of the batch (clamped: repeats are never used)
+    uint32_t w[SPW][2][BITS];
+    uint32_t sb[SPW][2];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      xs[m] = 0.f;
+    for (int j = 0; j < SPW; ++j) {
+      const int so = min(b0 + j, k_end - 1) * RB;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) dq[nb][m] = 0.f;
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int p = 0; p < FP; ++p) {
+          const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+          w[j][nb][4 * p] = v.x; w[j][nb][4 * p + 1] = v.y;
+          w[j][nb][4 * p + 2] = v.z; w[j][nb][4 * p + 3] = v.w;
+        }
+        if constexpr (RW == 1) {
+          w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+        } else if constexpr (RW == 2) {
+          const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
+          w[j][nb][4 * FP] = v.x; w[j][nb][4 * FP + 1] = v.y;
+        } else if constexpr (RW == 3) {
+          const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
+          w[j][nb][4 * FP] = v.x; w[j][nb][4 * FP + 1] = v.y; w[j][nb][4 * FP + 2] = v.z;
+        }
+        sb[j][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+      }
     }
-    // 4 chunks of 8 codes: 4 code pairs per unit against 4 activation pairs
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. everything of the batch has landed (correct whatever order the loads
+    //    were issued in); half-run sums: item t = (m, step, half) is the sum of
+    //    its four 16-byte chunks, one chunk per lane, met by two lane swaps
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t xv[MT][4];
+    for (int t0 = 0; t0 < NSUM * 4; t0 += 64) {
+      const int u = t0 + lane;                 // (item, chunk) = (u / 4, u % 4)
+      float v = 0.f;
+      if (u < NSUM * 4) {
+        const v4u_t c = *reinterpret_cast<const v4u_t*>(xw + u * 16);
+        v = dot2_bf16(c.x, 0x3F803F80u, dot2_bf16(c.y, 0x3F803F80u,
+            dot2_bf16(c.z, 0x3F803F80u, dot2_bf16(c.w, 0x3F803F80u, 0.f))));
+      }
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      if (u < NSUM * 4 && (u & 3) == 0) xsum[u / 4] = v;
+    }
+    __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      if (b0 + j >= k_end) break;
+      float dq[2][MT], xs[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const v4u_t v =
-            __builtin_amdgcn_raw_buffer_load_b128(xrs[m], xvo + c * 16, kk * 128, 0);
-        xv[m][0] = v.x; xv[m][1] = v.y; xv[m][2] = v.z; xv[m][3] = v.w;
+        xs[m] = xsum[(m * SPW + j) * 2 + g2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) dq[nb][m] = 0.f;
+      }
+      // 4 chunks of 8 codes: 4 code pairs per unit against 4 activation pairs
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        uint32_t xv[MT][4];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const v4u_t v = *reinterpret_cast<const v4u_t*>(xw + m * (SPW * 128) + j * 128 +
+                                                          g2 * 64 + c * 16);
+          xv[m][0] = v.x; xv[m][1] = v.y; xv[m][2] = v.z; xv[m][3] = v.w;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int q = 8 * c + 2 * i;
+            uint32_t pr;
+            if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
+              pr = pack_bf16x2(static_cast<float>(code_at<BITS>(w[j][nb], q)),
+                               static_cast<float>(code_at<BITS>(w[j][nb], q + 1)));
+            else
+              pr = (code_at<BITS>(w[j][nb], q) | (code_at<BITS>(w[j][nb], q + 1) << 16)) |
+                   0x43004300u;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) dq[nb][m] = dot2_bf16(pr, xv[m][i], dq[nb][m]);
+          }
       }
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
+      for (int nb = 0; nb < 2; ++nb) {
+        const float sc = __uint_as_float(sb[j][nb] << 16);
+        const float bi = __uint_as_float(sb[j][nb] & 0xFFFF0000u);
+        const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xs[m] = dot2_bf16(xv[m][j], 0x3F803F80u, xs[m]);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = 8 * c + 2 * j;
-          uint32_t pr;
-          if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
-            pr = pack_bf16x2(static_cast<float>(code_at<BITS>(w[nb], i)),
-                             static_cast<float>(code_at<BITS>(w[nb], i + 1)));
-          else
-            pr = (code_at<BITS>(w[nb], i) | (code_at<BITS>(w[nb], i + 1) << 16)) | 0x43004300u;
-#pragma unroll
-          for (int m = 0; m < MT; ++m) dq[nb][m] = dot2_bf16(pr, xv[m][j], dq[nb][m]);
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const float sc = __uint_as_float(sb[nb] << 16);
-      const float bi = __uint_as_float(sb[nb] & 0xFFFF0000u);
-      const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[nb][m] = fmaf(sc, dq[nb][m], fmaf(b2, xs[m], acc[nb][m]));
+        for (int m = 0; m < MT; ++m)
+          acc[nb][m] = fmaf(sc, dq[nb][m], fmaf(b2, xs[m], acc[nb][m]));
+      }
     }
   }
 
-  // the two code halves of each row meet across lanes l and l+32
+  // the two code halves of each row meet across lanes l and l+32; the waves'
+  // partials meet in LDS (each wave reuses its own activation region)
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[nb][m] += __shfl_xor(acc[nb][m], 32, 64);
+  float* part = reinterpret_cast<float*>(xw);
+  __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
   if (g2 == 0) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-      for (int m = 0; m < MT; ++m) part[wave][nb * 32 + l32][m] = acc[nb][m];
+      for (int m = 0; m < MT; ++m) part[(nb * 32 + l32) * MT + m] = acc[nb][m];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -381,7 +437,8 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     if (m >= mcount) break;
     float t = bv;
 #pragma unroll
-    for (int w = 0; w < WPB; ++w) t += part[w][lane][m];
+    for (int v = 0; v < WPB; ++v)
+      t += reinterpret_cast<const float*>(lds + v * XW)[lane * MT + m];
     y[static_cast<int64_t>(m0 + m) * N + n] = f32_to_bf16(t);
   }
 }
@@ -389,11 +446,12 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 template <int BITS, int MT>
 hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
                          const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  const int gs_log2 = gs == 32 ? 5 : (gs == 64 ? 6 : 7);
-  constexpr int WPB = 8;
   dim3 grid((N + 63) / 64, (M + MT - 1) / MT);
-  qmv_tiled_kernel<BITS, MT, WPB><<<grid, 64 * WPB, 0, s>>>(
-      x, M, K, static_cast<const uint8_t*>(tw), N, gs_log2, bias, y);
+  const uint8_t* t = static_cast<const uint8_t*>(tw);
+  if (gs == 32)
+    qmv_tiled_kernel<BITS, MT, 2><<<grid, 64 * kTiledWaves, 0, s>>>(x, M, K, t, N, bias, y);
+  else
+    qmv_tiled_kernel<BITS, MT, 1><<<grid, 64 * kTiledWaves, 0, s>>>(x, M, K, t, N, bias, y);
   return hipGetLastError();
 }
 
