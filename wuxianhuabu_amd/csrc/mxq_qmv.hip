@@ -251,34 +251,33 @@ typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTiledWaves = 16;  // waves per workgroup (one 64-row block)
-constexpr int kTiledSPW = 4;     // steps per wave per batch
-
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                          __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-template <int BITS, int MT, int GP>
-__global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
+// NH record halves (32 rows each) per workgroup of WPB waves; batches of SPW
+// steps per wave.
+template <int BITS, int MT, int GP, int NH, int WPB, int SPW>
+__global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
-  constexpr int WPB = kTiledWaves, SPW = kTiledSPW;
   constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
   constexpr int RB = tiled::code_bytes(BITS) + 256 * GP;      // record bytes
   // activation bytes per wave, a whole number of LDS-direct loads (64 lanes x
-  // 16 B each): the padding of MT = 1 receives repeats of a valid row
+  // 16 B each): the padding of small MT x SPW receives repeats of valid rows
   constexpr int XW = (MT * SPW * 128 + 1023) / 1024 * 1024;
   constexpr int XLOADS = XW / 1024;                           // LDS-direct loads per batch
   constexpr int NSUM = MT * SPW * 2;                          // half-run sums per batch
-  static_assert(64 * MT * 4 <= XW, "partials reuse the activation region");
+  static_assert(NH * 32 * MT * 4 <= XW, "partials reuse the activation region");
   __shared__ __attribute__((aligned(16))) uint8_t lds[WPB * XW];
   __shared__ float xsum_all[WPB][NSUM];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
-  const int rb = blockIdx.x;
+  const int rb = NH == 2 ? blockIdx.x : blockIdx.x >> 1;     // record row block
+  const int h0 = NH == 2 ? 0 : (blockIdx.x & 1);             // first half of this workgroup
   const int m0 = blockIdx.y * MT;
   const int mcount = min(MT, M - m0);
   const int nk = K >> 6;
@@ -289,20 +288,24 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
       tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
   const __amdgpu_buffer_rsrc_t xrs = ring::make_rsrc(
       x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(mcount) * K * 2);
-  int wvo[2], rvo[2], svo[2];
+  int wvo[NH], rvo[NH], svo[NH];
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    wvo[nb] = nb * tiled::half_bytes(BITS) + lane * 16;
-    rvo[nb] = nb * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
-    svo[nb] = tiled::code_bytes(BITS) + ((nb * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4;
+  for (int nb = 0; nb < NH; ++nb) {
+    const int h = h0 + nb;
+    wvo[nb] = h * tiled::half_bytes(BITS) + lane * 16;
+    rvo[nb] = h * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
+    svo[nb] = tiled::code_bytes(BITS) + ((h * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4;
   }
 
   const int per = (nk + WPB - 1) / WPB;
   const int k_begin = wave * per, k_end = min(nk, k_begin + per);
+  // pair_at's constants, in VGPRs
+  uint32_t kPairMask = ((1u << BITS) - 1u) * 0x10001u, kMagic = 0x43004300u;
+  asm volatile("" : "+v"(kPairMask), "+v"(kMagic));
 
-  float acc[2][MT];
+  float acc[NH][MT];
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
+  for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[nb][m] = 0.f;
 
@@ -320,14 +323,14 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
       ring::lds_load<16>(xrs, xw + i * 1024, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0);
     }
     asm volatile("" ::: "memory");  // the activation request stays ahead of the wait below
-    // 2. every weight record of the batch (clamped: repeats are never used)
-    uint32_t w[SPW][2][BITS];
-    uint32_t sb[SPW][2];
+    // 2. every weight unit of the batch (clamped: repeats are never used)
+    uint32_t w[SPW][NH][BITS];
+    uint32_t sb[SPW][NH];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int so = min(b0 + j, k_end - 1) * RB;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NH; ++nb) {
 #pragma unroll
         for (int p = 0; p < FP; ++p) {
           const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
@@ -368,12 +371,12 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       if (b0 + j >= k_end) break;
-      float dq[2][MT], xs[MT];
+      float dq[NH][MT], xs[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         xs[m] = xsum[(m * SPW + j) * 2 + g2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) dq[nb][m] = 0.f;
+        for (int nb = 0; nb < NH; ++nb) dq[nb][m] = 0.f;
       }
       // 4 chunks of 8 codes: 4 code pairs per unit against 4 activation pairs
 #pragma unroll
@@ -386,7 +389,7 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
           xv[m][0] = v.x; xv[m][1] = v.y; xv[m][2] = v.z; xv[m][3] = v.w;
         }
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int q = 8 * c + 2 * i;
@@ -395,14 +398,13 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
               pr = pack_bf16x2(static_cast<float>(code_at<BITS>(w[j][nb], q)),
                                static_cast<float>(code_at<BITS>(w[j][nb], q + 1)));
             else
-              pr = (code_at<BITS>(w[j][nb], q) | (code_at<BITS>(w[j][nb], q + 1) << 16)) |
-                   0x43004300u;
+              pr = pair_at<BITS>(w[j][nb], q, kPairMask, kMagic);
 #pragma unroll
             for (int m = 0; m < MT; ++m) dq[nb][m] = dot2_bf16(pr, xv[m][i], dq[nb][m]);
           }
       }
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NH; ++nb) {
         const float sc = __uint_as_float(sb[j][nb] << 16);
         const float bi = __uint_as_float(sb[j][nb] & 0xFFFF0000u);
         const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
@@ -416,20 +418,20 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
   // the two code halves of each row meet across lanes l and l+32; the waves'
   // partials meet in LDS (each wave reuses its own activation region)
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
+  for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[nb][m] += __shfl_xor(acc[nb][m], 32, 64);
   float* part = reinterpret_cast<float*>(xw);
   __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
   if (g2 == 0) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
       for (int m = 0; m < MT; ++m) part[(nb * 32 + l32) * MT + m] = acc[nb][m];
   }
   __syncthreads();
-  if (wave != 0) return;
-  const int n = rb * 64 + lane;
+  if (wave != 0 || lane >= NH * 32) return;
+  const int n = rb * 64 + h0 * 32 + lane;
   if (n >= N) return;
   const float bv = bias ? bf16_to_f32(bias[n]) : 0.f;
 #pragma unroll
@@ -443,15 +445,21 @@ __global__ __launch_bounds__(64 * kTiledWaves) void qmv_tiled_kernel(
   }
 }
 
+// Launch shape (measured best at M = 1, 2 and 8 for K = 4096, N = 24576 among
+// 1-2 halves x 4-16 waves x 4-8 steps): one workgroup per 32-row record half
+// (768 workgroups at N = 24576, three per CU), 8 waves, batches of 4 steps.
+constexpr int kTiledNH = 1, kTiledWaves = 8, kTiledSPW = 4;
+
 template <int BITS, int MT>
 hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
                          const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  dim3 grid((N + 63) / 64, (M + MT - 1) / MT);
+  constexpr int NH = kTiledNH, WPB = kTiledWaves, SPW = kTiledSPW;
+  dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
   const uint8_t* t = static_cast<const uint8_t*>(tw);
   if (gs == 32)
-    qmv_tiled_kernel<BITS, MT, 2><<<grid, 64 * kTiledWaves, 0, s>>>(x, M, K, t, N, bias, y);
+    qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW><<<grid, 64 * WPB, 0, s>>>(x, M, K, t, N, bias, y);
   else
-    qmv_tiled_kernel<BITS, MT, 1><<<grid, 64 * kTiledWaves, 0, s>>>(x, M, K, t, N, bias, y);
+    qmv_tiled_kernel<BITS, MT, 1, NH, WPB, SPW><<<grid, 64 * WPB, 0, s>>>(x, M, K, t, N, bias, y);
   return hipGetLastError();
 }
 
