@@ -86,28 +86,58 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
 
-  int m_tile, n_tile;
-  if (!ring::tile_coords<kGroupM>(m_tiles, n_tiles, m_tile, n_tile)) return;
-  const int m0 = m_tile * BM, n0 = n_tile * kRows;
+  // ---- persistent schedule: the tiles of the grouped order (see tile_of) are
+  // split into 8 contiguous ranges, one per XCD (workgroup b runs on XCD b % 8);
+  // the XCD's G/8 workgroups take its range round-robin, so in each round they
+  // hold consecutive tiles and share operands in that XCD's L2.
+  const int tiles = m_tiles * n_tiles;
+  const int per_xcd = gridDim.x >> 3;  // gridDim.x is a multiple of 8
+  const int t8 = (tiles + 7) >> 3;
+  const int first = (blockIdx.x & 7) * t8 + (blockIdx.x >> 3);
+  const int end = min(tiles, ((blockIdx.x & 7) + 1) * t8);
+  if (first >= end) return;
+  const int my_tiles = (end - first + per_xcd - 1) / per_xcd;
   const int nk = K >> 6;
-  const int rows_m = min(BM, M - m0);
-
-  const __amdgpu_buffer_rsrc_t xrs =
-      ring::make_rsrc(x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(rows_m) * K * 2);
-  // this wave's row block (clamped: a block past N computes rows never stored)
-  const int rb = min((n0 >> 6) + wave, (N + 63) / 64 - 1);
-  const __amdgpu_buffer_rsrc_t wrs = ring::make_rsrc(
-      tw + static_cast<int64_t>(rb) * nk * R::BYTES, static_cast<uint32_t>(nk) * R::BYTES);
+  const int row_blocks = (N + 63) >> 6;
+  // token / feature origin of this workgroup's r-th tile, packed as
+  // m0 * 65536 + n0 / 64 (m0 < 2^15 tokens... see the host's limits): groups of
+  // kGroupM token tiles sweep all feature tiles
+  auto tile_of = [&](int r) -> int64_t {
+    const int t = first + r * per_xcd;
+    const int per_group = kGroupM * n_tiles;
+    const int first_m = (t / per_group) * kGroupM;
+    const int gsize = min(m_tiles - first_m, kGroupM);
+    const int in_group = t % per_group;
+    const int64_t m0 = static_cast<int64_t>(first_m + in_group % gsize) * BM;
+    return (m0 << 32) | static_cast<uint32_t>((in_group / gsize) * kRows);
+  };
+  auto m0_of = [](int64_t t) { return static_cast<int>(t >> 32); };
+  auto n0_of = [](int64_t t) { return static_cast<int>(t & 0xFFFFFFFF); };
+  // activations of one token tile; rows past M lie outside the descriptor and
+  // load as zeros (their outputs are never stored)
+  auto x_rsrc = [&](int m0) {
+    return ring::make_rsrc(x + static_cast<int64_t>(m0) * K,
+                           static_cast<uint32_t>(min(BM, M - m0)) * K * 2);
+  };
+  // this wave's row block of one feature tile (clamped: a block past N computes
+  // rows that are never stored)
+  auto w_rsrc = [&](int n0) {
+    const int rb = min((n0 >> 6) + wave, row_blocks - 1);
+    return ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * R::BYTES,
+                           static_cast<uint32_t>(nk) * R::BYTES);
+  };
 
   // activation request i of this wave fills stage rows (wave*XL + i)*8 .. +8:
   // lane t writes physical chunk t%8 of row +t/8, i.e. logical chunk
-  // (t%8) ^ swz(row); rows past the tile repeat its last row
-  int xvo[XL];
+  // (t%8) ^ swz(row). The row's low 3 bits are t/8 and bit 3 is the parity of
+  // wave*XL + i, so the lane part of the offset takes two values (xvo) and the
+  // rest, (i & ~1) * 8 rows, is lane-independent (added to the scalar offset).
+  int xvo[2];
 #pragma unroll
-  for (int i = 0; i < XL; ++i) {
+  for (int i = 0; i < 2; ++i) {
     const int r = (wave * XL + i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ring::swz(r);
-    xvo[i] = (min(r, rows_m - 1) * K + 8 * c) * 2;
+    xvo[i] = (r * K + 8 * c) * 2;
   }
   // fragment reads: token row mb*32 + l32, logical chunk 4*g2 + sl
   int xro[4];
@@ -126,7 +156,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) wu[p][nb][i] = 0u;
-  // The third fill step (kk = -1) multiplies activation stage 2 by wu[0]; both
+  // The third fill step (g = -1) multiplies activation stage 2 by wu[0]; both
   // hold exact zeros then, so that step adds +0 whatever the inputs.
   {
     v4u* z = reinterpret_cast<v4u*>(xl + 2 * XSTAGE);
@@ -134,30 +164,39 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     for (int i = tid; i < XSTAGE / 16; i += kThreads) z[i] = v4u{0u, 0u, 0u, 0u};
   }
 
-  // request i of step kk (activations of step kk+2 first, needed a step
-  // sooner, then this wave's weight record of step kk+3); st = kk mod 3
-  auto request = [&](int i, int kk, int st) {
+  // Two request positions move through this workgroup's steps (tile r, K step
+  // k) ahead of the step being multiplied (g): activations (step g+2) and
+  // weights (step g+3). At the last step they stop and repeat it: a repeated
+  // request is harmless and keeps every step's request count equal. Plain
+  // scalars, advanced in place, so they stay in SGPRs.
+  int xs_r = 0, xs_k = 0, ws_r = 0, ws_k = 0;
+  int64_t xs_t = tile_of(0), ws_t = xs_t;
+
+  // request i of a step (activations first, needed a step sooner); st = the
+  // step's ring index g mod 3: activations of step g+2 go to stage (g+2) mod 3,
+  // weights of step g+3 to stage g mod 3
+  auto request = [&](int i, int st, const __amdgpu_buffer_rsrc_t& xr, int kx,
+                     const __amdgpu_buffer_rsrc_t& wr, int kw) __attribute__((always_inline)) {
     if (i < XL) {
-      const int kx = min(kk + 2, nk - 1);
-      const int stage = st == 0 ? 2 : st - 1;  // (kk + 2) mod 3
-      ring::lds_load<16>(xrs, xl + stage * XSTAGE + (wave * XL + i) * 1024, xvo[i], kx * 128);
+      const int stage = st == 0 ? 2 : st - 1;
+      ring::lds_load<16>(xr, xl + stage * XSTAGE + (wave * XL + i) * 1024, xvo[i & 1],
+                         kx * 128 + (i & ~1) * 16 * K);
     } else {
       const int j = i - XL;
-      const int kw = min(kk + 3, nk - 1);
-      const uint8_t* dst = wl + st * WSTAGE + wave * R::BYTES;  // (kk + 3) mod 3
+      const uint8_t* dst = wl + st * WSTAGE + wave * R::BYTES;
       if (j < R::CHUNKS) {
-        ring::lds_load<16>(wrs, dst + j * 1024, lane * 16, kw * R::BYTES + j * 1024);
+        ring::lds_load<16>(wr, dst + j * 1024, lane * 16, kw * R::BYTES + j * 1024);
       } else {
         const int off = R::CHUNKS * 1024 + (j - R::CHUNKS) * 256;
-        ring::lds_load<4>(wrs, dst + off, lane * 4, kw * R::BYTES + off);
+        ring::lds_load<4>(wr, dst + off, lane * 4, kw * R::BYTES + off);
       }
     }
   };
-  auto read_frag = [&](const uint8_t* stage, int q) {
+  auto read_frag = [&](const uint8_t* stage, int q) __attribute__((always_inline)) {
     return *reinterpret_cast<const bf16x8*>(stage + (q / 4) * 4096 + xro[q % 4]);
   };
   // this lane's two runs of one record, from LDS
-  auto read_raw = [&](const uint8_t* rec, RawRun<BITS>& r) {
+  auto read_raw = [&](const uint8_t* rec, RawRun<BITS>& r) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const uint8_t* h = rec + nb * R::HALF;
@@ -182,13 +221,75 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
           rec + R::CODE + ((nb * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4);
     }
   };
+  // ---- epilogue of one tile: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3)
+  // for one token m. One 32 x 32 accumulator block at a time (fenced, so the
+  // block's 16 values are the only accumulators read out at once), each block
+  // restarting at zero after its stores.
+  auto store_tile = [&](int m0, int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int nl = n0 + wave * 64 + nb * 32 + 4 * g2;  // feature of (a, r) = nl + 8a + r
+      float bv[4][4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bv[a][r] = bias && nl + 8 * a + r < N ? bf16_to_f32(bias[nl + 8 * a + r]) : 0.f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = m0 + mb * 32 + l32;
+        const f32x16 c = acc[nb][mb];
+        if (m < M) {
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const int n = nl + 8 * a;
+            uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
+            const float v0 = c[4 * a] + bv[a][0], v1 = c[4 * a + 1] + bv[a][1];
+            const float v2 = c[4 * a + 2] + bv[a][2], v3 = c[4 * a + 3] + bv[a][3];
+            if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
+              *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+            } else {
+              const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (n + r < N) dst[r] = f32_to_bf16(v[r]);
+            }
+          }
+        }
+        acc[nb][mb] = f32x16{};
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
 
-  // One K step; J = parity of kk + 3 selects the unpack buffers, st = kk mod 3
-  // the ring stages. Fill steps (kk = -3, -2) only request; from kk = -1 on the
-  // step also reads step kk+1's record, multiplies step kk and unpacks kk+1.
-  auto step = [&](auto Jc, int kk, int st) {
+  // One K step g (st = g mod 3; J = g & 1 selects the unpack buffers). FULL
+  // steps also read step g+1's record, multiply step g and unpack step g+1;
+  // the first two fill steps (g = -3, -2) only request. Requests are spread
+  // over the MFMA pairs.
+  auto step = [&](auto Jc, auto fullc, int g, int st) __attribute__((always_inline)) {
     constexpr int J = decltype(Jc)::value;
-    if (kk >= -1) {
+    constexpr bool FULL = decltype(fullc)::value;
+    // this step's requests: activations (none before step 0), weights
+    const __amdgpu_buffer_rsrc_t xr = x_rsrc(m0_of(xs_t)), wr = w_rsrc(n0_of(ws_t));
+    const int kx = xs_k, kw = ws_k;
+    const bool x_on = g >= -2;
+    if (x_on && ++xs_k == nk) {
+      if (xs_r + 1 < my_tiles) {
+        xs_k = 0;
+        xs_t = tile_of(++xs_r);
+      } else {
+        xs_k = nk - 1;
+      }
+    }
+    if (++ws_k == nk) {
+      if (ws_r + 1 < my_tiles) {
+        ws_k = 0;
+        ws_t = tile_of(++ws_r);
+      } else {
+        ws_k = nk - 1;
+      }
+    }
+    if constexpr (FULL) {
       const uint8_t* xb = xl + st * XSTAGE;
       const uint8_t* wb = wl + (st == 2 ? 0 : st + 1) * WSTAGE + wave * R::BYTES;
       bf16x8 f[4];
@@ -205,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       for (int q = 0; q < SLOTS; ++q) {
 #pragma unroll
         for (int i = 0; i < L; ++i)
-          if (i * SLOTS / L == q) request(i, kk, st);
+          if (i * SLOTS / L == q) request(i, st, xr, kx, wr, kw);
         if (q + 3 < SLOTS) f[(q + 3) % 4] = read_frag(xb, q + 3);
         const int mb = q / 4, sl = q % 4;
 #pragma unroll
@@ -232,62 +333,70 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     } else {
 #pragma unroll
       for (int i = 0; i < L; ++i)
-        if (i >= XL || kk >= -2) request(i, kk, st);  // no activations of step -1
+        if (i >= XL || x_on) request(i, st, xr, kx, wr, kw);
     }
     // every request older than this step's own has landed, for all waves
     ring::ring_barrier<L>();
   };
+  using J0 = std::integral_constant<int, 0>;
+  using J1 = std::integral_constant<int, 1>;
+  using Full = std::true_type;
+  using Fill = std::false_type;
 
   ring::ring_barrier<0>();  // stage 2 zeroed by all waves
-  for (int kk = -3, st = 0;;) {
-    step(std::integral_constant<int, 0>{}, kk, st);
-    if (++kk >= nk) break;
+  // fill: g = -3, -2 request; g = -1 (st = 2, wu[1] = 0) also unpacks step 0
+  step(J1{}, Fill{}, -3, 0);
+  step(J0{}, Fill{}, -2, 1);
+  step(J1{}, Full{}, -1, 2);
+  // tiles: the epilogue stays out of the step loop; a tile with an odd number
+  // of K steps leaves the next one starting on the other unpack parity
+  int g = 0, st = 0;
+  auto next = [&] __attribute__((always_inline)) {
+    ++g;
     st = st == 2 ? 0 : st + 1;
-    step(std::integral_constant<int, 1>{}, kk, st);
-    if (++kk >= nk) break;
-    st = st == 2 ? 0 : st + 1;
+  };
+  for (int r = 0; r < my_tiles; ++r) {
+    int left = nk;
+    if (g & 1) {
+      step(J1{}, Full{}, g, st);
+      next();
+      --left;
+    }
+    for (; left >= 2; left -= 2) {
+      step(J0{}, Full{}, g, st);
+      next();
+      step(J1{}, Full{}, g, st);
+      next();
+    }
+    if (left) {
+      step(J0{}, Full{}, g, st);
+      next();
+    }
+    const int64_t t = tile_of(r);
+    store_tile(m0_of(t), n0_of(t));
   }
-  // the last steps' requests (repeats of step nk-1) must land before the
+  // the last steps' requests (repeats of the last step) must land before the
   // workgroup's LDS is released
   ring::wait_vmcnt<0>();
+}
 
-  // ---- epilogue: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3) for one token m ----
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int n = n0 + wave * 64 + nb * 32 + 8 * a + 4 * g2;
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bv[r] = n + r < N ? bf16_to_f32(bias[n + r]) : 0.f;
-      }
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int m = m0 + mb * 32 + l32;
-        if (m >= M) continue;
-        uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
-        const f32x16 c = acc[nb][mb];
-        const float v0 = c[4 * a] + bv[0], v1 = c[4 * a + 1] + bv[1];
-        const float v2 = c[4 * a + 2] + bv[2], v3 = c[4 * a + 3] + bv[3];
-        if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
-          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-        } else {
-          const float v[4] = {v0, v1, v2, v3};
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) dst[r] = f32_to_bf16(v[r]);
-        }
-      }
-    }
-  }
+// One workgroup per CU (rounded to whole XCD sets), never more than the tiles.
+inline int persistent_blocks(int tiles) {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 256;
+    return n;
+  }();
+  return ring::grid_blocks(min(tiles, cus));
 }
 
 template <int BITS, int BM, int GP>
 hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
   const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + kRows - 1) / kRows;
-  qmm_tiled_kernel<BITS, BM, GP><<<ring::grid_blocks(m_tiles * n_tiles), kThreads, 0, s>>>(
+  qmm_tiled_kernel<BITS, BM, GP><<<persistent_blocks(m_tiles * n_tiles), kThreads, 0, s>>>(
       x, static_cast<const uint8_t*>(tw), bias, y, M, N, K, m_tiles, n_tiles);
   return hipGetLastError();
 }
