@@ -15,7 +15,7 @@ import torch
 
 import wuxianhuabu_amd as mx
 from tests.gpu_util import (assert_tight, dev_bf16, dev_words, host_bf16, host_f32_of_bf16,
-                            spec_metric)
+                            host_words, spec_metric)
 from tests.test_gpu_matmul import make_case
 
 pytestmark = pytest.mark.gpu
@@ -73,6 +73,28 @@ def test_tiled_qmm_bit_identical_to_mlx_layout(dev, O, bits, gs, M, K):
     rows = np.arange(0, M, 7)
     ref = O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows)
     assert_tight(host_f32_of_bf16(y_t)[rows], ref, f"tiled qmm bits={bits} gs={gs}")
+
+
+@pytest.mark.parametrize("bits,gs", [(6, 64), (4, 32), (3, 64)])
+@pytest.mark.parametrize("K", [576, 640])
+def test_tiled_qmm_several_tiles_per_workgroup(dev, O, bits, gs, K):
+    """More tiles than workgroups (9 x 33 = 297 tiles of 256 x 256), ragged in M and N,
+    with an odd (576 / 64 = 9) and an even number of K steps: the persistent kernel carries
+    its load streams and unpack parity across tile boundaries."""
+    M, N = 2100, 8200
+    g = torch.Generator(device=dev)
+    g.manual_seed(bits * 1000 + K)
+    x = torch.randn(M, K, generator=g, device=dev).bfloat16()
+    w = torch.randn(N, K, generator=g, device=dev) * 0.02
+    bias = (torch.randn(N, generator=g, device=dev) * 0.1).bfloat16()
+    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16)
+    y_t = mx.tiled_matmul(x, mx.tile(wq, s, b, gs, bits), bias=bias, path="qmm")
+    y_m = mx.quantized_matmul(x, wq, s, b, group_size=gs, bits=bits, bias=bias, path="qmm")
+    assert torch.equal(y_t, y_m), f"bits={bits} gs={gs} K={K}: tiled and MLX-layout differ"
+    rows = np.array([0, 255, 256, 1023, 2047, 2048, M - 1])
+    ref = O.qmm_f64_bf16w(host_bf16(x[torch.as_tensor(rows, device=dev)]), host_words(wq),
+                          host_bf16(s), host_bf16(b), gs, bits, bias=host_bf16(bias), threads=16)
+    assert_tight(host_f32_of_bf16(y_t)[rows], ref, f"tiled qmm bits={bits} gs={gs} K={K}")
 
 
 @pytest.mark.parametrize("M,N,K", [(9, 64, 64), (33, 1, 128), (64, 130, 192), (65, 200, 320),

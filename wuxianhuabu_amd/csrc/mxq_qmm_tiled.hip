@@ -63,7 +63,7 @@ struct RawRun {  // one lane's two 32-code runs and their scale/bias dwords
   uint32_t sb[2];
 };
 
-template <int BITS, int BM, int GP>
+template <int BITS, int BM, int GP, bool EVEN>
 __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ tw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
@@ -326,6 +326,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
             wu[J ^ 1][nb][i] =
                 pack_bf16x2(fmaf(static_cast<float>(code_at<BITS>(raw.w[nb], 2 * i)), sc, bi),
                             fmaf(static_cast<float>(code_at<BITS>(raw.w[nb], 2 * i + 1)), sc, bi));
+            // pinned here: otherwise the compiler sinks the unpack into the next
+            // step (its only user), doubling that step's VALU work
+            asm volatile("" : "+v"(wu[J ^ 1][nb][i]));
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -348,8 +351,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   step(J1{}, Fill{}, -3, 0);
   step(J0{}, Fill{}, -2, 1);
   step(J1{}, Full{}, -1, 2);
-  // tiles: the epilogue stays out of the step loop; a tile with an odd number
-  // of K steps leaves the next one starting on the other unpack parity
+  // tiles: the epilogue stays out of the step loop. With an even number of K
+  // steps (EVEN) every tile starts on unpack parity 0; otherwise a tile with an
+  // odd count leaves the next one starting on the other parity.
   int g = 0, st = 0;
   auto next = [&] __attribute__((always_inline)) {
     ++g;
@@ -357,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   };
   for (int r = 0; r < my_tiles; ++r) {
     int left = nk;
-    if (g & 1) {
+    if (!EVEN && (g & 1)) {
       step(J1{}, Full{}, g, st);
       next();
       --left;
@@ -368,7 +372,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       step(J1{}, Full{}, g, st);
       next();
     }
-    if (left) {
+    if (!EVEN && left) {
       step(J0{}, Full{}, g, st);
       next();
     }
@@ -396,8 +400,14 @@ template <int BITS, int BM, int GP>
 hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
   const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + kRows - 1) / kRows;
-  qmm_tiled_kernel<BITS, BM, GP><<<persistent_blocks(m_tiles * n_tiles), kThreads, 0, s>>>(
-      x, static_cast<const uint8_t*>(tw), bias, y, M, N, K, m_tiles, n_tiles);
+  const int blocks = persistent_blocks(m_tiles * n_tiles);
+  const uint8_t* w = static_cast<const uint8_t*>(tw);
+  if ((K >> 6) % 2 == 0)
+    qmm_tiled_kernel<BITS, BM, GP, true><<<blocks, kThreads, 0, s>>>(x, w, bias, y, M, N, K,
+                                                                     m_tiles, n_tiles);
+  else
+    qmm_tiled_kernel<BITS, BM, GP, false><<<blocks, kThreads, 0, s>>>(x, w, bias, y, M, N, K,
+                                                                      m_tiles, n_tiles);
   return hipGetLastError();
 }
 
