@@ -43,6 +43,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));  // y is 4-byte aligned
 
 // One wave's record (64 rows x 64 codes) of the tiled layout, and how it is
 // moved: CHUNKS loads of 1 KiB (16 B per lane), then TAIL loads of 256 B.
@@ -221,44 +222,78 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
           rec + R::CODE + ((nb * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4);
     }
   };
-  // ---- epilogue of one tile: lane holds y[m, n + 8a + 4*g2 + r] (a, r = 0..3)
-  // for one token m. One 32 x 32 accumulator block at a time (fenced, so the
-  // block's 16 values are the only accumulators read out at once), each block
-  // restarting at zero after its stores.
-  auto store_tile = [&](int m0, int n0) __attribute__((always_inline)) {
+  // ---- epilogue of one tile, one 32-token block (mb) at a time: the lane holds
+  // y[m0 + 32 mb + l32, n + nb*32 + 8a + 4*g2 + r] (a, r = 0..3, n = n0 + 64*wave).
+  // The wave rounds its 32 x 64 block to bf16 (bias added in fp32 first) into
+  // LDS, reads it back as 16-byte row pieces and stores 8 full 128-byte row
+  // segments per instruction. The staging area is this wave's own part of the
+  // activation stage the tile's last step consumed: after that step's barrier no
+  // wave reads it, and only this wave's requests of the next step write it.
+  auto store_tile = [&](int m0, int n0, uint8_t* stage) __attribute__((always_inline)) {
+    uint8_t* const sb = stage + wave * XL * 1024;  // >= 4 KiB, 16-byte aligned
+    const int nw = n0 + wave * 64;
+    // lane-derived offsets are recomputed per tile (a few VALU) rather than
+    // hoisted out of the tile loop, where they would be live across the steps
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int l32 = ln & 31, g2 = ln >> 5;
+    // the lane's 32 bias values as bf16 pairs (features 2j, 2j+1 of its runs)
+    uint32_t bp[2][4][2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int nl = n0 + wave * 64 + nb * 32 + 4 * g2;  // feature of (a, r) = nl + 8a + r
-      float bv[4][4];
+    for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bv[a][r] = bias && nl + 8 * a + r < N ? bf16_to_f32(bias[nl + 8 * a + r]) : 0.f;
+        for (int h = 0; h < 2; ++h) {
+          const int n = nw + nb * 32 + 8 * a + 4 * g2 + 2 * h;
+          const uint32_t lo = bias && n < N ? bias[n] : 0u;
+          const uint32_t hi = bias && n + 1 < N ? bias[n + 1] : 0u;
+          bp[nb][a][h] = lo | (hi << 16);
+        }
+    auto bias_at = [&](int nb, int a, int r) __attribute__((always_inline)) {
+      const uint32_t w = bp[nb][a][r >> 1];
+      return __uint_as_float((r & 1) ? (w & 0xFFFF0000u) : (w << 16));
+    };
+    // read-back position: row rr = 8 i + lane / 8, 16-byte chunk lane % 8
+    const int cr = ln & 7, rr0 = ln >> 3;
+    const int n = nw + 8 * cr;
+    const bool vec = n + 8 <= N;
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int m = m0 + mb * 32 + l32;
-        const f32x16 c = acc[nb][mb];
-        if (m < M) {
+    for (int mb = 0; mb < MB; ++mb) {
+      if (m0 + mb * 32 < M) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
-            const int n = nl + 8 * a;
-            uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
-            const float v0 = c[4 * a] + bv[a][0], v1 = c[4 * a + 1] + bv[a][1];
-            const float v2 = c[4 * a + 2] + bv[a][2], v3 = c[4 * a + 3] + bv[a][3];
-            if (n + 3 < N && ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0)) {
-              *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
-            } else {
-              const float v[4] = {v0, v1, v2, v3};
+            const f32x16 c = acc[nb][mb];
+            const int chunk = (nb * 4 + a) ^ (l32 & 7);
+            *reinterpret_cast<v2u*>(sb + l32 * 128 + chunk * 16 + g2 * 8) =
+                v2u{pack_bf16x2(c[4 * a] + bias_at(nb, a, 0), c[4 * a + 1] + bias_at(nb, a, 1)),
+                    pack_bf16x2(c[4 * a + 2] + bias_at(nb, a, 2),
+                                c[4 * a + 3] + bias_at(nb, a, 3))};
+          }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the block is in LDS
 #pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (n + r < N) dst[r] = f32_to_bf16(v[r]);
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 8 * i + rr0;
+          const v4u v = *reinterpret_cast<const v4u*>(sb + rr * 128 + ((cr ^ (rr & 7)) * 16));
+          const int m = m0 + mb * 32 + rr;
+          if (m < M) {
+            uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
+            if (vec && (reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
+              *reinterpret_cast<u32x4*>(dst) = u32x4{v.x, v.y, v.z, v.w};
+            } else {
+              const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                if (n + e < N) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
             }
           }
         }
-        acc[nb][mb] = f32x16{};
-        __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[nb][mb] = f32x16{};
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -377,7 +412,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       next();
     }
     const int64_t t = tile_of(r);
-    store_tile(m0_of(t), n0_of(t));
+    store_tile(m0_of(t), n0_of(t), xl + (st == 0 ? 2 : st - 1) * XSTAGE);
   }
   // the last steps' requests (repeats of the last step) must land before the
   // workgroup's LDS is released
