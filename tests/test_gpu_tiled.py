@@ -77,11 +77,13 @@ def test_tiled_qmm_bit_identical_to_mlx_layout(dev, O, bits, gs, M, K):
 
 @pytest.mark.parametrize("bits,gs", [(6, 64), (4, 32), (3, 64)])
 @pytest.mark.parametrize("K", [576, 640])
-def test_tiled_qmm_several_tiles_per_workgroup(dev, O, bits, gs, K):
-    """More tiles than workgroups (9 x 33 = 297 tiles of 256 x 256), ragged in M and N,
-    with an odd (576 / 64 = 9) and an even number of K steps: the persistent kernel carries
-    its load streams and unpack parity across tile boundaries."""
-    M, N = 2100, 8200
+@pytest.mark.parametrize("M,N", [(2100, 8200), (2100, 8192), (2148, 8192)])
+def test_tiled_qmm_several_tiles_per_workgroup(dev, O, bits, gs, K, M, N):
+    """More tiles than CUs, ragged in M (and N), with an odd (576 / 64 = 9) and an even
+    number of K steps: the persistent kernel carries its load streams and unpack parity
+    across tile boundaries. On a 256-CU device, 2100 x 8200 runs 9 x 33 tiles of 256 rows
+    in one launch; 2100 x 8192 (8 x 32 full tiles) and 2148 x 8192 move the 52- and
+    100-row remainders to a second launch of 64- and 128-row tiles."""
     g = torch.Generator(device=dev)
     g.manual_seed(bits * 1000 + K)
     x = torch.randn(M, K, generator=g, device=dev).bfloat16()

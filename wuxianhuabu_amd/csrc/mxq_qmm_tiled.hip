@@ -77,8 +77,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   constexpr int L = XL + R::LOADS;     // requests per wave per step
   constexpr int SLOTS = MB * 4;        // MFMA pairs per step
   static_assert(L <= SLOTS, "one request per MFMA pair at most");
-  static_assert(kStages * (XSTAGE + WSTAGE) <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * (XSTAGE + WSTAGE)];
+  // epilogue staging: 4 KiB per wave, inside the consumed activation stage when
+  // the wave's part of it is that large (BM >= 128), else a separate area
+  constexpr bool OWN_STAGING = XL * 1024 < 4096;
+  constexpr int LDS_BYTES = kStages * (XSTAGE + WSTAGE) + (OWN_STAGING ? 4 * 4096 : 0);
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
   uint8_t* const xl = lds;
   uint8_t* const wl = lds + kStages * XSTAGE;
 
@@ -228,9 +232,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   // LDS, reads it back as 16-byte row pieces and stores 8 full 128-byte row
   // segments per instruction. The staging area is this wave's own part of the
   // activation stage the tile's last step consumed: after that step's barrier no
-  // wave reads it, and only this wave's requests of the next step write it.
+  // wave reads it, and only this wave's requests of the next step write it
+  // (with BM = 64 that part is too small and the block goes to its own area).
   auto store_tile = [&](int m0, int n0, uint8_t* stage) __attribute__((always_inline)) {
-    uint8_t* const sb = stage + wave * XL * 1024;  // >= 4 KiB, 16-byte aligned
+    uint8_t* const sb = OWN_STAGING ? lds + kStages * (XSTAGE + WSTAGE) + wave * 4096
+                                    : stage + wave * XL * 1024;  // 16-byte aligned
     const int nw = n0 + wave * 64;
     // lane-derived offsets are recomputed per tile (a few VALU) rather than
     // hoisted out of the tile loop, where they would be live across the steps
@@ -419,8 +425,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   ring::wait_vmcnt<0>();
 }
 
-// One workgroup per CU (rounded to whole XCD sets), never more than the tiles.
-inline int persistent_blocks(int tiles) {
+inline int cu_count() {
   static int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -428,8 +433,11 @@ inline int persistent_blocks(int tiles) {
       n = 256;
     return n;
   }();
-  return ring::grid_blocks(min(tiles, cus));
+  return cus;
 }
+
+// One workgroup per CU (rounded to whole XCD sets), never more than the tiles.
+inline int persistent_blocks(int tiles) { return ring::grid_blocks(min(tiles, cu_count())); }
 
 template <int BITS, int BM, int GP>
 hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
@@ -446,15 +454,44 @@ hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
   return hipGetLastError();
 }
 
+// Time of one 64- or 128-token tile relative to a 256-token tile (same K, same
+// 256 features): the weight loads and unpacking do not shrink with the tile.
+constexpr double kTileCost64 = 0.6, kTileCost128 = 0.75;
+
+// Token tiles of 256 rows (64 or 128 for small M). When M % 256 leaves a
+// remainder of at most 128 rows and the full tiles alone fill whole rounds of
+// the CUs better, the remainder runs as a second launch with smaller tiles
+// instead of as a last round of mostly empty 256-row tiles.
+template <int BITS, int GP>
+hipError_t pick_rows(const uint16_t* x, int M, int K, const void* tw, int N,
+                     const uint16_t* bias, uint16_t* y, hipStream_t s) {
+  if (M <= 64) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, y, s);
+  if (M <= 128) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, y, s);
+  const int full = M / 256, rem = M % 256;
+  if (rem > 0 && rem <= 128) {
+    const int64_t cus = cu_count(), n_tiles = (N + kRows - 1) / kRows;
+    const int64_t t_full = static_cast<int64_t>(full) * n_tiles;
+    const double one = static_cast<double>((t_full + n_tiles + cus - 1) / cus);
+    const double two = static_cast<double>((t_full + cus - 1) / cus) +
+                       static_cast<double>((n_tiles + cus - 1) / cus) *
+                           (rem <= 64 ? kTileCost64 : kTileCost128);
+    if (two < one) {
+      const hipError_t e = run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, y, s);
+      if (e != hipSuccess) return e;
+      const int64_t r0 = static_cast<int64_t>(full) * 256;
+      if (rem <= 64)
+        return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, y + r0 * N, s);
+      return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, y + r0 * N, s);
+    }
+  }
+  return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, y, s);
+}
+
 template <int BITS>
 hipError_t pick_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
                       const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  if (gs == 32) {
-    if (M <= 128) return run_tiled<BITS, 128, 2>(x, M, K, tw, N, bias, y, s);
-    return run_tiled<BITS, 256, 2>(x, M, K, tw, N, bias, y, s);
-  }
-  if (M <= 128) return run_tiled<BITS, 128, 1>(x, M, K, tw, N, bias, y, s);
-  return run_tiled<BITS, 256, 1>(x, M, K, tw, N, bias, y, s);
+  if (gs == 32) return pick_rows<BITS, 2>(x, M, K, tw, N, bias, y, s);
+  return pick_rows<BITS, 1>(x, M, K, tw, N, bias, y, s);
 }
 
 }  // namespace
