@@ -227,29 +227,32 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 
 // ---------------------------------------------------------------------------
 // GEMV on the tiled layout (mxq_tiled.hpp). HBM-bound, so the design goal is
-// bytes in flight: one workgroup of 16 waves per 64-row block; the waves split
-// the block's K steps into contiguous spans (the block's records are
-// contiguous in HBM). Each wave, per batch of up to SPW steps:
+// bytes in flight with as little VALU work per byte as possible: one
+// workgroup of a few waves per 32-row record half; the waves split the K steps
+// into contiguous spans (a row block's records are contiguous in HBM). Each
+// wave, per batch of up to SPW steps:
 //   1. moves its activation slice (MT rows x SPW steps x 128 B) into its own
 //      LDS region with LDS-direct loads (no other wave reads it: no barrier);
-//   2. issues every weight load of the batch at once (SPW records of 64 rows x
-//      64 codes: 13 KB per wave at 6-bit, several hundred KB per CU);
-//   3. waits for the batch, sums each activation half-run once (32 codes of a
-//      row per lane half; the sums are shared by the 32 lanes of the half), and
-//      consumes the records. Sixteen waves per workgroup overlap one another's
-//      loads and arithmetic.
-// Per step a lane owns two units (rows r and r+32 of the block, code half g):
-// 2 x 32 codes from coalesced 16-byte planes.
+//   2. issues every weight load of the batch at once;
+//   3. waits for the batch, sums each activation half-run once, and consumes
+//      the records.
+// Per step a lane owns one unit (row l32 of the half, code half g2): 32 codes
+// from a coalesced 16-byte plane plus remainder words.
 //
 // Codes become bf16 pairs without float arithmetic: 0x4300 | q is the bf16
-// value 128 + q for q < 128, so a pair of codes (2i, 2i+1) in one dword meets
-// the raw bf16 activation pair (x[2i], x[2i+1]) in v_dot2_f32_bf16. Per unit,
+// value 128 + q for q < 128. The dot products run on the matrix cores: per
+// step, four v_mfma_f32_32x32x16_bf16 with the activations as A (rows = tokens,
+// zero past M) and the code pairs as B (columns = the 32 rows of the half).
+// Operand lane l supplies K slots 8*(l/32) .. +7 of MFMA c; both operands map
+// slot (g2, c, j) to code 32*g2 + 8c + j of the step, so the MFMA sums the
+// step's 64 codes. Lane (l32, g2) then holds tokens 4*g2 .. 4*g2+3 of row l32:
 //   sum_k x_k (s q_k + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k.
 // 8-bit codes (up to 255) are converted exactly instead, with offset 0.
 // ---------------------------------------------------------------------------
 typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
@@ -257,11 +260,12 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 // NH record halves (32 rows each) per workgroup of WPB waves; batches of SPW
-// steps per wave.
+// steps per wave; MT <= 8 tokens.
 template <int BITS, int MT, int GP, int NH, int WPB, int SPW>
 __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+  static_assert(MT <= 8, "a lane half holds 4 tokens of the MFMA output");
   constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
   constexpr int RB = tiled::code_bytes(BITS) + 256 * GP;      // record bytes
   // activation bytes per wave, a whole number of LDS-direct loads (64 lanes x
@@ -269,8 +273,10 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   constexpr int XW = (MT * SPW * 128 + 1023) / 1024 * 1024;
   constexpr int XLOADS = XW / 1024;                           // LDS-direct loads per batch
   constexpr int NSUM = MT * SPW * 2;                          // half-run sums per batch
+  constexpr int RPL = MT < 4 ? MT : 4;                        // tokens per lane half
   static_assert(NH * 32 * MT * 4 <= XW, "partials reuse the activation region");
   __shared__ __attribute__((aligned(16))) uint8_t lds[WPB * XW];
+  __shared__ __attribute__((aligned(16))) uint8_t zero_chunk[WPB][SPW * 128];
   __shared__ float xsum_all[WPB][NSUM];
 
   const int lane = threadIdx.x & 63;
@@ -294,8 +300,20 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const int h = h0 + nb;
     wvo[nb] = h * tiled::half_bytes(BITS) + lane * 16;
     rvo[nb] = h * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
-    svo[nb] = tiled::code_bytes(BITS) + ((h * 32 + l32) * GP + (GP == 2 ? g2 : 0)) * 4;
+    svo[nb] = tiled::code_bytes(BITS) + (h * 32 + l32) * GP * 4;  // both groups if GP == 2
   }
+  // A operand rows: token l32 of the batch's activations, zeros past MT. With
+  // two groups per step (GP == 2) each code half gets its own MFMA set, whose A
+  // is zero in the other half's K slots.
+  {
+    v4u_t* z = reinterpret_cast<v4u_t*>(zero_chunk[wave]);
+    for (int i = lane; i < SPW * 8; i += 64) z[i] = v4u_t{0u, 0u, 0u, 0u};
+  }
+  const uint8_t* xa[GP];
+#pragma unroll
+  for (int e = 0; e < GP; ++e)
+    xa[e] = (l32 < MT && (GP == 1 || g2 == e) ? xw + l32 * (SPW * 128) : zero_chunk[wave]) +
+            g2 * 64;
 
   const int per = (nk + WPB - 1) / WPB;
   const int k_begin = wave * per, k_end = min(nk, k_begin + per);
@@ -303,11 +321,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   uint32_t kPairMask = ((1u << BITS) - 1u) * 0x10001u, kMagic = 0x43004300u;
   asm volatile("" : "+v"(kPairMask), "+v"(kMagic));
 
-  float acc[NH][MT];
+  float acc[NH][RPL];
 #pragma unroll
   for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[nb][m] = 0.f;
+    for (int r = 0; r < RPL; ++r) acc[nb][r] = 0.f;
 
   for (int b0 = k_begin; b0 < k_end; b0 += SPW) {
     // 1. activations of steps b0 .. b0+SPW-1 (clamped; rows past M repeat a
@@ -325,7 +343,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     asm volatile("" ::: "memory");  // the activation request stays ahead of the wait below
     // 2. every weight unit of the batch (clamped: repeats are never used)
     uint32_t w[SPW][NH][BITS];
-    uint32_t sb[SPW][NH];
+    uint32_t sb[SPW][NH][GP];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int so = min(b0 + j, k_end - 1) * RB;
@@ -346,7 +364,13 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
           w[j][nb][4 * FP] = v.x; w[j][nb][4 * FP + 1] = v.y; w[j][nb][4 * FP + 2] = v.z;
         }
-        sb[j][nb] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+        if constexpr (GP == 2) {
+          const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, svo[nb], so, 0);
+          sb[j][nb][0] = v.x;
+          sb[j][nb][GP - 1] = v.y;
+        } else {
+          sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -371,64 +395,69 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       if (b0 + j >= k_end) break;
-      float dq[NH][MT], xs[MT];
+      // step sums of this lane's tokens 4*g2 + r (zero past MT), per group
+      float xs[GP][RPL];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        xs[m] = xsum[(m * SPW + j) * 2 + g2];
-#pragma unroll
-        for (int nb = 0; nb < NH; ++nb) dq[nb][m] = 0.f;
-      }
-      // 4 chunks of 8 codes: 4 code pairs per unit against 4 activation pairs
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        uint32_t xv[MT][4];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const v4u_t v = *reinterpret_cast<const v4u_t*>(xw + m * (SPW * 128) + j * 128 +
-                                                          g2 * 64 + c * 16);
-          xv[m][0] = v.x; xv[m][1] = v.y; xv[m][2] = v.z; xv[m][3] = v.w;
+      for (int r = 0; r < RPL; ++r) {
+        const int m = 4 * g2 + r, mc = min(m, MT - 1);
+        const float h0s = xsum[(mc * SPW + j) * 2], h1s = xsum[(mc * SPW + j) * 2 + 1];
+        if constexpr (GP == 2) {
+          xs[0][r] = m < MT ? h0s : 0.f;
+          xs[GP - 1][r] = m < MT ? h1s : 0.f;
+        } else {
+          xs[0][r] = m < MT ? h0s + h1s : 0.f;
         }
+      }
+      bf16x8 av[GP][4];
 #pragma unroll
-        for (int nb = 0; nb < NH; ++nb)
+      for (int e = 0; e < GP; ++e)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          av[e][c] = *reinterpret_cast<const bf16x8*>(xa[e] + j * 128 + c * 16);
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) {
+        bf16x8 bv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          uint32_t pr[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int q = 8 * c + 2 * i;
-            uint32_t pr;
             if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
-              pr = pack_bf16x2(static_cast<float>(code_at<BITS>(w[j][nb], q)),
-                               static_cast<float>(code_at<BITS>(w[j][nb], q + 1)));
+              pr[i] = pack_bf16x2(static_cast<float>(code_at<BITS>(w[j][nb], q)),
+                                  static_cast<float>(code_at<BITS>(w[j][nb], q + 1)));
             else
-              pr = pair_at<BITS>(w[j][nb], q, kPairMask, kMagic);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) dq[nb][m] = dot2_bf16(pr, xv[m][i], dq[nb][m]);
+              pr[i] = pair_at<BITS>(w[j][nb], q, kPairMask, kMagic);
           }
-      }
+          bv[c] = __builtin_bit_cast(bf16x8, v4u_t{pr[0], pr[1], pr[2], pr[3]});
+        }
 #pragma unroll
-      for (int nb = 0; nb < NH; ++nb) {
-        const float sc = __uint_as_float(sb[j][nb] << 16);
-        const float bi = __uint_as_float(sb[j][nb] & 0xFFFF0000u);
-        const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
+        for (int e = 0; e < GP; ++e) {
+          f32x16_t d;
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-          acc[nb][m] = fmaf(sc, dq[nb][m], fmaf(b2, xs[m], acc[nb][m]));
+          for (int c = 0; c < 4; ++c)
+            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[e][c], bv[c], c == 0 ? f32x16_t{} : d,
+                                                        0, 0, 0);
+          const float sc = __uint_as_float(sb[j][nb][e] << 16);
+          const float bi = __uint_as_float(sb[j][nb][e] & 0xFFFF0000u);
+          const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
+#pragma unroll
+          for (int r = 0; r < RPL; ++r)
+            acc[nb][r] = fmaf(sc, d[r], fmaf(b2, xs[e][r], acc[nb][r]));
+        }
       }
     }
   }
 
-  // the two code halves of each row meet across lanes l and l+32; the waves'
-  // partials meet in LDS (each wave reuses its own activation region)
+  // the waves' partials meet in LDS (each wave reuses its own activation
+  // region): lane (l32, g2) holds tokens 4*g2 + r of row l32
+  float* part = reinterpret_cast<float*>(xw);
+  __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
 #pragma unroll
   for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[nb][m] += __shfl_xor(acc[nb][m], 32, 64);
-  float* part = reinterpret_cast<float*>(xw);
-  __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-  if (g2 == 0) {
-#pragma unroll
-    for (int nb = 0; nb < NH; ++nb)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) part[(nb * 32 + l32) * MT + m] = acc[nb][m];
-  }
+    for (int r = 0; r < RPL; ++r)
+      if (4 * g2 + r < MT) part[(nb * 32 + l32) * MT + 4 * g2 + r] = acc[nb][r];
   __syncthreads();
   if (wave != 0 || lane >= NH * 32) return;
   const int n = rb * 64 + h0 * 32 + lane;
@@ -446,9 +475,9 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 }
 
 // Launch shape (measured best at M = 1, 2 and 8 for K = 4096, N = 24576 among
-// 1-2 halves x 4-16 waves x 4-8 steps): one workgroup per 32-row record half
-// (768 workgroups at N = 24576, three per CU), 8 waves, batches of 4 steps.
-constexpr int kTiledNH = 1, kTiledWaves = 8, kTiledSPW = 4;
+// 1-2 halves x 2-16 waves x 2-16 steps): one workgroup per 32-row record half
+// (768 workgroups at N = 24576, three per CU), 4 waves, batches of 4 steps.
+constexpr int kTiledNH = 1, kTiledWaves = 4, kTiledSPW = 4;
 
 template <int BITS, int MT>
 hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
