@@ -296,6 +296,43 @@ def main():
     print(f"[bench] qmm: avg {avg_ms:.3f} ms  median {med_ms:.3f} ms  "
           f"{achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
+    # ---------------- fused epilogues on the same workload ----------------
+    # GELU-tanh (LTX feed-forward) and silu(gate) * up (H3 MLP, the weight's rows read as
+    # [gate; up] and tiled in pairs) in the qmm's epilogue, against the unfused chain:
+    # the same qmm writing bf16, then torch's elementwise activation on it.
+    fused_steps = max(5, steps // 3)
+    tw_pairs = mx.tile(wq, s, b, c["gs"], c["bits"], swiglu=True)
+    half = c["N"] // 2
+    y_half = torch.empty(c["M"], half, dtype=torch.bfloat16, device=dev)
+
+    def fused_launch(act, t, out):
+        def f(_i):
+            ok(L.mxq_qmm_tiled_act(P(x), c["M"], c["K"], P(t.data), c["N"], c["gs"],
+                                   c["bits"], None, act, P(out), cur()))
+        return f
+
+    def gelu_unfused(_i):
+        qmm_launch(_i)
+        torch.nn.functional.gelu(y, approximate="tanh")
+
+    def swiglu_unfused(_i):
+        qmm_launch(_i)
+        torch.mul(torch.nn.functional.silu(y[:, :half]), y[:, half:], out=y_half)
+
+    fused = {}
+    for name, fn_f, fn_u in (("gelu_tanh", fused_launch(1, tw, y), gelu_unfused),
+                             ("swiglu", fused_launch(2, tw_pairs, y_half), swiglu_unfused)):
+        pf, _ = time_launches(torch, fn_f, fused_steps, 2)
+        pu, _ = time_launches(torch, fn_u, fused_steps, 2)
+        af, au = sum(pf) / len(pf), sum(pu) / len(pu)
+        fused[name] = {"fused_ms": af, "unfused_ms": au,
+                       "fused_tflops": flop / (af * 1e-3) / 1e12}
+        print(f"[bench] {name}: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
+              flush=True)
+    res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation",
+                             **fused}
+    del tw_pairs, y_half
+
     # ---------------- gemv ----------------
     g = GEMV
     gx, gwq, gs_, gb = make_inputs(torch, mx, g, dev)

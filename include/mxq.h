@@ -148,6 +148,35 @@ int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_
 int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
                   int group_size, int bits, const void* bias, void* y, mxq_stream stream);
 
+/* ---- activations fused into the tiled MFMA kernel's epilogue ---------------
+ * The activation is applied to x*W^T + bias in fp32, before the single bf16
+ * rounding, so the pre-activation [M, N] never goes to memory. */
+#define MXQ_ACT_NONE 0
+#define MXQ_ACT_GELU_TANH 1 /* 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) */
+#define MXQ_ACT_SWIGLU 2    /* silu(gate) * up, weights tiled by mxq_tile_swiglu */
+
+/* Tiled layout of an [N, K] weight whose rows are [gate; up] (N even, N/2 rows
+ * each): record row block rb holds gate rows 32rb .. 32rb+31 in its first half
+ * and the matching up rows N/2 + 32rb .. N/2 + 32rb+31 in its second, so that
+ * one lane holds both operands of silu(gate) * up. Same size as
+ * mxq_tiled_bytes(N, ...). Serves the fused fc1 of the H3 MLP, whose output the
+ * reference splits in halves and combines as silu(gate) * up
+ * (`model/minimax h3/H3Transformer.swift:620-629`). */
+int mxq_tile_swiglu(const uint32_t* wq, const void* scales, const void* biases, int64_t N,
+                    int64_t K, int group_size, int bits, void* tiled, mxq_stream stream);
+
+/* y = act(x * W^T + bias) on the MFMA kernel, any M >= 0:
+ *   MXQ_ACT_NONE       as mxq_qmm_tiled;
+ *   MXQ_ACT_GELU_TANH  weights from mxq_tile; y [M, N]. Replaces
+ *                      geluApprox(proj_in(x)) between the LTX feed-forward
+ *                      projections (`model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:392-401`);
+ *   MXQ_ACT_SWIGLU     weights from mxq_tile_swiglu, N even, bias [N] (gate
+ *                      half, then up half); y [M, N/2] = silu(gate) * up
+ *                      (`model/minimax h3/H3Transformer.swift:620-629`). */
+int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                      int group_size, int bits, const void* bias, int act, void* y,
+                      mxq_stream stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* mxq_last_error(void);
 

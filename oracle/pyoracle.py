@@ -230,3 +230,49 @@ def gelu_tanh_bf16(a):
     out = np.empty(a.shape, np.uint16)
     lib().orc_gelu_tanh_bf16(a.reshape(-1), a.size, out.reshape(-1))
     return out
+
+
+# ---------------------------------------------------------------- fused activations (fp64)
+def gelu_tanh_f64(a):
+    """0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) in fp64: mlx's geluApproximate, applied
+    to the LTX feed-forward's first projection (`model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:392-401`)."""
+    v = np.asarray(a, np.float64)
+    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+
+
+def silu_f64(a):
+    """v * sigmoid(v) in fp64."""
+    v = np.asarray(a, np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def swiglu_f64(y):
+    """silu(gate) * up of a fused fc1 output y [..., 2F] whose halves are gate and up
+    (`model/minimax h3/H3Transformer.swift:620-629`: splitEqual(y, 2, axis 1), silu(h0) * h1)."""
+    y = np.asarray(y, np.float64)
+    F = y.shape[-1] // 2
+    return silu_f64(y[..., :F]) * y[..., F:]
+
+
+def swiglu_rows(N):
+    """Source row of each row of the paired tiling of an [N, K] gate/up weight (N even):
+    row block rb holds rows 32rb.. of the gate half, then rows N/2 + 32rb.. of the up half;
+    -1 marks the zero rows that pad a half past N/2."""
+    F = N // 2
+    nb = (F + 31) // 32
+    rows = np.full(nb * 64, -1, np.int64)
+    for rb in range(nb):
+        for r in range(32):
+            j = rb * 32 + r
+            if j < F:
+                rows[rb * 64 + r] = j
+                rows[rb * 64 + 32 + r] = F + j
+    return rows
+
+
+def tile_swiglu(wq, scales, biases, K, gs, bits):
+    """The paired tiling: tile() of the row-permuted triple (zero rows for the padding)."""
+    wq, scales, biases = _c(wq, np.uint32), _c(scales, np.uint16), _c(biases, np.uint16)
+    rows = swiglu_rows(wq.shape[0])
+    pick = lambda a: np.where((rows >= 0)[:, None], a[np.maximum(rows, 0)], 0).astype(a.dtype)
+    return tile(pick(wq), pick(scales), pick(biases), K, gs, bits)

@@ -10,7 +10,7 @@ Device memory and streams come from torch; every kernel lives in libmxq.so,
 whose C ABI is include/mxq.h.
 """
 from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
-from .nn import MfLinear, QuantizedLinear  # noqa: F401
+from .nn import H3MlpW, LTXFFN, MfLinear, QuantizedLinear  # noqa: F401
 from .ops import (TiledWeight, dequantized, pack, quantized, quantized_matmul,  # noqa: F401
                   quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401

@@ -21,6 +21,9 @@ MXQ_BFLOAT16 = 1
 MXQ_MODE_MINMAX = 0
 MXQ_MODE_MLX_EDGE = 1
 MXQ_QMV_MAX_M = 8
+MXQ_ACT_NONE = 0
+MXQ_ACT_GELU_TANH = 1
+MXQ_ACT_SWIGLU = 2
 ABI_VERSION = 1
 
 # every symbol include/mxq.h declares, with (restype, argtypes)
@@ -36,9 +39,11 @@ SIGNATURES = {
     "mxq_qmv": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),
     "mxq_tile": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
+    "mxq_tile_swiglu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
     "mxq_quantized_matmul_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp,
                                           _vp]),
     "mxq_qmm_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
+    "mxq_qmm_tiled_act": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _int, _vp, _vp]),
     "mxq_qmv_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_last_error": (ctypes.c_char_p, []),
     "mxq_status_string": (ctypes.c_char_p, [_int]),

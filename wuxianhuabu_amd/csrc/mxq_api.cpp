@@ -249,10 +249,15 @@ int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits) {
   return mxq::tiled::total_bytes(N, K, group_size, bits);
 }
 
-int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
-             int group_size, int bits, void* tiled, mxq_stream stream) {
+namespace {
+int tile_impl(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
+              int group_size, int bits, bool pairs, void* tiled, mxq_stream stream) {
   const int64_t bytes = mxq_tiled_bytes(N, K, group_size, bits);
   if (bytes < 0) return static_cast<int>(bytes);
+  if (pairs && N % 2 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[tile] A SwiGLU weight needs an even number of rows (gate, then up; got %lld).",
+                static_cast<long long>(N));
   if (N == 0 || K == 0) return ok();
   if (!wq || !scales || !biases || !tiled)
     return fail(MXQ_ERR_NULL, "[tile] w, scales, biases and tiled must be non-NULL.");
@@ -263,7 +268,18 @@ int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t
   return hip_status("tile", mxq::detail::launch_tile(
                                 wq, static_cast<const uint16_t*>(scales),
                                 static_cast<const uint16_t*>(biases), N, K, group_size, bits,
-                                tiled, static_cast<hipStream_t>(stream)));
+                                pairs, tiled, static_cast<hipStream_t>(stream)));
+}
+}  // namespace
+
+int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
+             int group_size, int bits, void* tiled, mxq_stream stream) {
+  return tile_impl(wq, scales, biases, N, K, group_size, bits, false, tiled, stream);
+}
+
+int mxq_tile_swiglu(const uint32_t* wq, const void* scales, const void* biases, int64_t N,
+                    int64_t K, int group_size, int bits, void* tiled, mxq_stream stream) {
+  return tile_impl(wq, scales, biases, N, K, group_size, bits, true, tiled, stream);
 }
 
 namespace {
@@ -292,17 +308,30 @@ int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void*
 }
 }  // namespace
 
-int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
-                  int group_size, int bits, const void* bias, void* y, mxq_stream stream) {
+int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                      int group_size, int bits, const void* bias, int act, void* y,
+                      mxq_stream stream) {
   int rc = check_tiled("quantized_matmul", x, M, K, tiled, N, group_size, bits, bias, y);
   if (rc) return rc;
+  if (act != MXQ_ACT_NONE && act != MXQ_ACT_GELU_TANH && act != MXQ_ACT_SWIGLU)
+    return fail(MXQ_ERR_INVALID, "[quantized_matmul] Unknown activation %d.", act);
+  if (act == MXQ_ACT_SWIGLU && N % 2 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[quantized_matmul] SwiGLU needs an even number of weight rows (got %lld).",
+                static_cast<long long>(N));
   if (M == 0 || N == 0) return ok();
   return hip_status("quantized_matmul",
                     mxq::detail::launch_qmm_tiled(
                         static_cast<const uint16_t*>(x), static_cast<int>(M),
                         static_cast<int>(K), tiled, static_cast<int>(N), group_size, bits,
-                        static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                        static_cast<const uint16_t*>(bias), act, static_cast<uint16_t*>(y),
                         static_cast<hipStream_t>(stream)));
+}
+
+int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                  int group_size, int bits, const void* bias, void* y, mxq_stream stream) {
+  return mxq_qmm_tiled_act(x, M, K, tiled, N, group_size, bits, bias, MXQ_ACT_NONE, y,
+                           stream);
 }
 
 int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,

@@ -21,8 +21,11 @@ hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void*
                              void* out, int out_dtype, hipStream_t s);
 
 // MLX layout -> tiled layout (mxq_tiled.hpp). K % 64 == 0, bf16 scales/biases.
+// With `pairs`, row block rb takes rows 32rb.. (first half) and N/2 + 32rb..
+// (second half) of an [N, K] weight with N even.
 hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
-                       int64_t N, int64_t K, int gs, int bits, void* out, hipStream_t s);
+                       int64_t N, int64_t K, int gs, int bits, bool pairs, void* out,
+                       hipStream_t s);
 
 // y[M,N] = x[M,K] * W^T (+ bias): small-M split-K GEMV (any M; rows of x are
 // processed in blocks of up to 8).
@@ -39,8 +42,10 @@ bool qmm_supports_bits(int bits);
 
 // Both kernels on tiled weights (K % 64 == 0): any M for the MFMA kernel,
 // M <= 8 for the GEMV.
+// act: MXQ_ACT_* (mxq.h), applied in the MFMA kernel's epilogue.
 hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
-                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
+                            int bits, const uint16_t* bias, int act, uint16_t* y,
+                            hipStream_t s);
 hipError_t launch_qmv_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
                             int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
 

@@ -167,6 +167,7 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
                                                         const uint16_t* __restrict__ scales,
                                                         const uint16_t* __restrict__ biases,
                                                         int64_t N, int64_t K, int gs,
+                                                        bool pairs,
                                                         uint8_t* __restrict__ out) {
   const int64_t nk = K / 64;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -177,8 +178,10 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
   const int64_t rk = idx >> 7;  // rb * nk + kk
   const int64_t rb = rk / nk, kk = rk - rb * nk;
   const int r = u & 31, g = u >> 5;
-  const int64_t row = rb * 64 + h * 32 + r;
-  const bool valid = row < N;
+  // source row of tiled row rb*64 + h*32 + r; with `pairs`, the halves of row
+  // block rb are rows 32rb + r and N/2 + 32rb + r (gate and up of one output)
+  const int64_t row = pairs ? h * (N / 2) + rb * 32 + r : rb * 64 + h * 32 + r;
+  const bool valid = pairs ? rb * 32 + r < N / 2 : row < N;
   const int64_t W = K / 32 * BITS;
   uint32_t words[BITS];
   const uint32_t* src = wq + (valid ? row : 0) * W + (kk * 64 + 32 * g) / 32 * BITS;
@@ -213,10 +216,10 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
 template <int BITS>
 struct TileRun {
   static hipError_t run(const uint32_t* wq, const uint16_t* sc, const uint16_t* bi, int64_t N,
-                        int64_t K, int gs, void* out, hipStream_t s) {
+                        int64_t K, int gs, bool pairs, void* out, hipStream_t s) {
     const int64_t items = tiled::row_blocks(N) * (K / 64) * 128;
     if (items == 0) return hipSuccess;
-    tile_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, sc, bi, N, K, gs,
+    tile_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, sc, bi, N, K, gs, pairs,
                                                            static_cast<uint8_t*>(out));
     return hipGetLastError();
   }
@@ -330,8 +333,9 @@ hipError_t launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t col
 }
 
 hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
-                       int64_t N, int64_t K, int gs, int bits, void* out, hipStream_t s) {
-  return by_bits<TileRun>(bits, wq, scales, biases, N, K, gs, out, s);
+                       int64_t N, int64_t K, int gs, int bits, bool pairs, void* out,
+                       hipStream_t s) {
+  return by_bits<TileRun>(bits, wq, scales, biases, N, K, gs, pairs, out, s);
 }
 
 hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,

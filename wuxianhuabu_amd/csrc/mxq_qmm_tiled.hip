@@ -26,6 +26,7 @@
 // request but step k's own L has landed) then a workgroup barrier.
 #include <type_traits>
 
+#include "mxq.h"
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
 #include "mxq_ring.hpp"
@@ -58,6 +59,24 @@ struct Rec {
   static constexpr int LOADS = CHUNKS + TAIL;
 };
 
+// Activations fused into the epilogue (values in fp32, before the one bf16
+// rounding): GELU with the tanh approximation
+// 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), as between the LTX
+// feed-forward projections (`model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:392-401`),
+// and silu(v) = v / (1 + e^{-v}) for silu(gate) * up on the fused fc1 output of
+// the H3 MLP (`model/minimax h3/H3Transformer.swift:620-629`). Since
+// 0.5 (1 + tanh(u)) = 1 / (1 + e^{-2u}), both are v / (1 + e^{-z}): one exp2
+// and one reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each, far below the
+// bf16 rounding that follows). e^{-z} = inf gives -0 / +0 in the limits.
+__device__ __forceinline__ float act_sigmoid_times(float v, float z) {
+  return __fdividef(v, 1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));
+}
+__device__ __forceinline__ float act_gelu_tanh(float v) {
+  const float u = 0.7978845608028654f * fmaf(0.044715f * v, v * v, v);
+  return act_sigmoid_times(v, 2.f * u);
+}
+__device__ __forceinline__ float act_silu(float v) { return act_sigmoid_times(v, v); }
+
 template <int BITS>
 struct RawRun {  // one lane's two 32-code runs and their scale/bias dwords
   uint32_t w[2][BITS];
@@ -68,7 +87,7 @@ template <int BITS, int BM, int GP, bool EVEN>
 __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ tw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
-    int m_tiles, int n_tiles) {
+    int m_tiles, int n_tiles, int act) {
   using R = Rec<BITS, GP>;
   constexpr int MB = BM / 32;          // 32-token blocks per wave
   constexpr int XL = BM / 32;          // activation requests per wave per step (8 rows each)
@@ -227,23 +246,33 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     }
   };
   // ---- epilogue of one tile, one 32-token block (mb) at a time: the lane holds
-  // y[m0 + 32 mb + l32, n + nb*32 + 8a + 4*g2 + r] (a, r = 0..3, n = n0 + 64*wave).
-  // The wave rounds its 32 x 64 block to bf16 (bias added in fp32 first) into
-  // LDS, reads it back as 16-byte row pieces and stores 8 full 128-byte row
-  // segments per instruction. The staging area is this wave's own part of the
-  // activation stage the tile's last step consumed: after that step's barrier no
-  // wave reads it, and only this wave's requests of the next step write it
-  // (with BM = 64 that part is too small and the block goes to its own area).
-  auto store_tile = [&](int m0, int n0, uint8_t* stage) __attribute__((always_inline)) {
+  // acc for features n + nb*32 + 8a + 4*g2 + r (a, r = 0..3, n = n0 + 64*wave)
+  // of token m0 + 32 mb + l32. The wave rounds its block to bf16 (bias added and
+  // the activation applied in fp32 first) into LDS, reads it back as 16-byte row
+  // pieces and stores whole row segments: 128 B (64 features) per row, or 64 B
+  // for SwiGLU, whose record halves are the gate and up rows of the same 32
+  // outputs (tiled by mxq_tile_swiglu) and whose output row has N/2 columns.
+  // The staging area is this wave's own part of the activation stage the tile's
+  // last step consumed: after that step's barrier no wave reads it, and only
+  // this wave's requests of the next step write it (with BM = 64 that part is
+  // too small and the block goes to its own area).
+  auto store_tile = [&](auto actc, int m0, int n0, uint8_t* stage) __attribute__((always_inline)) {
+    constexpr int ACT = decltype(actc)::value;
+    constexpr bool GLU = ACT == MXQ_ACT_SWIGLU;
+    constexpr int ROWB = GLU ? 64 : 128;  // staged bytes per token row
+    constexpr int CPR = ROWB / 16;        // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;         // rows per read-back instruction
     uint8_t* const sb = OWN_STAGING ? lds + kStages * (XSTAGE + WSTAGE) + wave * 4096
                                     : stage + wave * XL * 1024;  // 16-byte aligned
-    const int nw = n0 + wave * 64;
+    const int ncol = GLU ? N / 2 : N;                            // output columns
+    const int c0 = GLU ? n0 / 2 + wave * 32 : n0 + wave * 64;    // this wave's first
     // lane-derived offsets are recomputed per tile (a few VALU) rather than
     // hoisted out of the tile loop, where they would be live across the steps
     int ln;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
     const int l32 = ln & 31, g2 = ln >> 5;
-    // the lane's 32 bias values as bf16 pairs (features 2j, 2j+1 of its runs)
+    // the lane's 32 bias values as bf16 pairs (features 2j, 2j+1 of its runs);
+    // SwiGLU: gate bias [0, N/2), up bias [N/2, N)
     uint32_t bp[2][4][2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
@@ -251,48 +280,69 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int n = nw + nb * 32 + 8 * a + 4 * g2 + 2 * h;
-          const uint32_t lo = bias && n < N ? bias[n] : 0u;
-          const uint32_t hi = bias && n + 1 < N ? bias[n + 1] : 0u;
+          const int j = 8 * a + 4 * g2 + 2 * h;
+          const int n = GLU ? (nb ? ncol : 0) + c0 + j : c0 + nb * 32 + j;
+          const int lim = GLU ? (nb ? N : ncol) : N;
+          const uint32_t lo = bias && n < lim ? bias[n] : 0u;
+          const uint32_t hi = bias && n + 1 < lim ? bias[n + 1] : 0u;
           bp[nb][a][h] = lo | (hi << 16);
         }
     auto bias_at = [&](int nb, int a, int r) __attribute__((always_inline)) {
       const uint32_t w = bp[nb][a][r >> 1];
       return __uint_as_float((r & 1) ? (w & 0xFFFF0000u) : (w << 16));
     };
-    // read-back position: row rr = 8 i + lane / 8, 16-byte chunk lane % 8
-    const int cr = ln & 7, rr0 = ln >> 3;
-    const int n = nw + 8 * cr;
-    const bool vec = n + 8 <= N;
+    // read-back position: row rr = RPI i + lane / CPR, 16-byte chunk lane % CPR
+    const int cr = ln % CPR, rr0 = ln / CPR;
+    const int n = c0 + 8 * cr;
+    const bool vec = n + 8 <= ncol;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       if (m0 + mb * 32 < M) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        if constexpr (GLU) {
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
-            const f32x16 c = acc[nb][mb];
-            const int chunk = (nb * 4 + a) ^ (l32 & 7);
-            *reinterpret_cast<v2u*>(sb + l32 * 128 + chunk * 16 + g2 * 8) =
-                v2u{pack_bf16x2(c[4 * a] + bias_at(nb, a, 0), c[4 * a + 1] + bias_at(nb, a, 1)),
-                    pack_bf16x2(c[4 * a + 2] + bias_at(nb, a, 2),
-                                c[4 * a + 3] + bias_at(nb, a, 3))};
+            const f32x16 cg = acc[0][mb], cu = acc[1][mb];
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              o[r] = act_silu(cg[4 * a + r] + bias_at(0, a, r)) * (cu[4 * a + r] + bias_at(1, a, r));
+            const int chunk = a ^ (l32 & 3);
+            *reinterpret_cast<v2u*>(sb + l32 * 64 + chunk * 16 + g2 * 8) =
+                v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
+        } else {
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+              const f32x16 c = acc[nb][mb];
+              float o[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                o[r] = c[4 * a + r] + bias_at(nb, a, r);
+                if constexpr (ACT == MXQ_ACT_GELU_TANH) o[r] = act_gelu_tanh(o[r]);
+              }
+              const int chunk = (nb * 4 + a) ^ (l32 & 7);
+              *reinterpret_cast<v2u*>(sb + l32 * 128 + chunk * 16 + g2 * 8) =
+                  v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            }
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the block is in LDS
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = 8 * i + rr0;
-          const v4u v = *reinterpret_cast<const v4u*>(sb + rr * 128 + ((cr ^ (rr & 7)) * 16));
+        for (int i = 0; i < 32 / RPI; ++i) {
+          const int rr = RPI * i + rr0;
+          const v4u v =
+              *reinterpret_cast<const v4u*>(sb + rr * ROWB + ((cr ^ (rr & (CPR - 1))) * 16));
           const int m = m0 + mb * 32 + rr;
           if (m < M) {
-            uint16_t* dst = y + static_cast<int64_t>(m) * N + n;
+            uint16_t* dst = y + static_cast<int64_t>(m) * ncol + n;
             if (vec && (reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
               *reinterpret_cast<u32x4*>(dst) = u32x4{v.x, v.y, v.z, v.w};
             } else {
               const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
               for (int e = 0; e < 8; ++e)
-                if (n + e < N) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+                if (n + e < ncol) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
             }
           }
         }
@@ -418,7 +468,13 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       next();
     }
     const int64_t t = tile_of(r);
-    store_tile(m0_of(t), n0_of(t), xl + (st == 0 ? 2 : st - 1) * XSTAGE);
+    uint8_t* const stage = xl + (st == 0 ? 2 : st - 1) * XSTAGE;
+    if (act == MXQ_ACT_GELU_TANH)
+      store_tile(std::integral_constant<int, MXQ_ACT_GELU_TANH>{}, m0_of(t), n0_of(t), stage);
+    else if (act == MXQ_ACT_SWIGLU)
+      store_tile(std::integral_constant<int, MXQ_ACT_SWIGLU>{}, m0_of(t), n0_of(t), stage);
+    else
+      store_tile(std::integral_constant<int, MXQ_ACT_NONE>{}, m0_of(t), n0_of(t), stage);
   }
   // the last steps' requests (repeats of the last step) must land before the
   // workgroup's LDS is released
@@ -441,16 +497,16 @@ inline int persistent_blocks(int tiles) { return ring::grid_blocks(min(tiles, cu
 
 template <int BITS, int BM, int GP>
 hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
-                     const uint16_t* bias, uint16_t* y, hipStream_t s) {
+                     const uint16_t* bias, int act, uint16_t* y, hipStream_t s) {
   const int m_tiles = (M + BM - 1) / BM, n_tiles = (N + kRows - 1) / kRows;
   const int blocks = persistent_blocks(m_tiles * n_tiles);
   const uint8_t* w = static_cast<const uint8_t*>(tw);
   if ((K >> 6) % 2 == 0)
     qmm_tiled_kernel<BITS, BM, GP, true><<<blocks, kThreads, 0, s>>>(x, w, bias, y, M, N, K,
-                                                                     m_tiles, n_tiles);
+                                                                     m_tiles, n_tiles, act);
   else
     qmm_tiled_kernel<BITS, BM, GP, false><<<blocks, kThreads, 0, s>>>(x, w, bias, y, M, N, K,
-                                                                      m_tiles, n_tiles);
+                                                                      m_tiles, n_tiles, act);
   return hipGetLastError();
 }
 
@@ -464,9 +520,9 @@ constexpr double kTileCost64 = 0.6, kTileCost128 = 0.75;
 // instead of as a last round of mostly empty 256-row tiles.
 template <int BITS, int GP>
 hipError_t pick_rows(const uint16_t* x, int M, int K, const void* tw, int N,
-                     const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  if (M <= 64) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, y, s);
-  if (M <= 128) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, y, s);
+                     const uint16_t* bias, int act, uint16_t* y, hipStream_t s) {
+  if (M <= 64) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, y, s);
+  if (M <= 128) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, y, s);
   const int full = M / 256, rem = M % 256;
   if (rem > 0 && rem <= 128) {
     const int64_t cus = cu_count(), n_tiles = (N + kRows - 1) / kRows;
@@ -476,22 +532,23 @@ hipError_t pick_rows(const uint16_t* x, int M, int K, const void* tw, int N,
                        static_cast<double>((n_tiles + cus - 1) / cus) *
                            (rem <= 64 ? kTileCost64 : kTileCost128);
     if (two < one) {
-      const hipError_t e = run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, y, s);
+      const hipError_t e = run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, act, y, s);
       if (e != hipSuccess) return e;
       const int64_t r0 = static_cast<int64_t>(full) * 256;
+      const int64_t ldy = act == MXQ_ACT_SWIGLU ? N / 2 : N;
       if (rem <= 64)
-        return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, y + r0 * N, s);
-      return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, y + r0 * N, s);
+        return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, act, y + r0 * ldy, s);
+      return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, act, y + r0 * ldy, s);
     }
   }
-  return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, y, s);
+  return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, act, y, s);
 }
 
 template <int BITS>
 hipError_t pick_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
-                      const uint16_t* bias, uint16_t* y, hipStream_t s) {
-  if (gs == 32) return pick_rows<BITS, 2>(x, M, K, tw, N, bias, y, s);
-  return pick_rows<BITS, 1>(x, M, K, tw, N, bias, y, s);
+                      const uint16_t* bias, int act, uint16_t* y, hipStream_t s) {
+  if (gs == 32) return pick_rows<BITS, 2>(x, M, K, tw, N, bias, act, y, s);
+  return pick_rows<BITS, 1>(x, M, K, tw, N, bias, act, y, s);
 }
 
 }  // namespace
@@ -499,15 +556,16 @@ hipError_t pick_tiled(const uint16_t* x, int M, int K, const void* tw, int N, in
 namespace detail {
 
 hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
-                            int bits, const uint16_t* bias, uint16_t* y, hipStream_t s) {
+                            int bits, const uint16_t* bias, int act, uint16_t* y,
+                            hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   switch (bits) {
-    case 2: return pick_tiled<2>(x, M, K, tw, N, gs, bias, y, s);
-    case 3: return pick_tiled<3>(x, M, K, tw, N, gs, bias, y, s);
-    case 4: return pick_tiled<4>(x, M, K, tw, N, gs, bias, y, s);
-    case 5: return pick_tiled<5>(x, M, K, tw, N, gs, bias, y, s);
-    case 6: return pick_tiled<6>(x, M, K, tw, N, gs, bias, y, s);
-    case 8: return pick_tiled<8>(x, M, K, tw, N, gs, bias, y, s);
+    case 2: return pick_tiled<2>(x, M, K, tw, N, gs, bias, act, y, s);
+    case 3: return pick_tiled<3>(x, M, K, tw, N, gs, bias, act, y, s);
+    case 4: return pick_tiled<4>(x, M, K, tw, N, gs, bias, act, y, s);
+    case 5: return pick_tiled<5>(x, M, K, tw, N, gs, bias, act, y, s);
+    case 6: return pick_tiled<6>(x, M, K, tw, N, gs, bias, act, y, s);
+    case 8: return pick_tiled<8>(x, M, K, tw, N, gs, bias, act, y, s);
     default: return hipErrorInvalidValue;
   }
 }

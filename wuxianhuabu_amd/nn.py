@@ -175,3 +175,70 @@ class MfLinear:
         return out
 
     __call__ = forward
+
+
+class LTXFFN:
+    """The LTX feed-forward (`model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:372-401`):
+    proj_in -> geluApprox -> proj_out, two QuantizedLinear. With tiled weights the GELU runs
+    in proj_in's epilogue (fp32, before the one bf16 rounding), so the [M, ffnDim]
+    pre-activation never goes to memory. The IC-LoRA side paths of the reference are not
+    part of this path."""
+
+    def __init__(self, dim, ffn_dim, bias=True, group_size=64, bits=4, device="cuda",
+                 seed=None, tiled=True):
+        self.dim, self.ffn_dim = int(dim), int(ffn_dim)
+        self.proj_in = QuantizedLinear(dim, ffn_dim, bias, group_size, bits, device,
+                                       None if seed is None else seed, tiled)
+        self.proj_out = QuantizedLinear(ffn_dim, dim, bias, group_size, bits, device,
+                                        None if seed is None else seed + 1, tiled)
+
+    def __call__(self, x):
+        tw = self.proj_in.tiled_weight()
+        if tw is not None and x.dtype == torch.bfloat16 and x.shape[-1] == tw.K:
+            mid = ops.tiled_matmul(x, tw, bias=self.proj_in.bias, activation="gelu_tanh")
+        else:
+            mid = torch.nn.functional.gelu(self.proj_in(x).float(),
+                                           approximate="tanh").to(torch.bfloat16)
+        return self.proj_out(mid)
+
+    callAsFunction = __call__
+
+
+class H3MlpW:
+    """The H3 MLP (`model/minimax h3/H3Transformer.swift:601-629`): fc1 [S, hidden] ->
+    [S, 2*ffn] (gate and up fused), silu(gate) * up, fc2. When fc1 is quantized and
+    tileable its weight is tiled once in gate/up pairs (mxq_tile_swiglu) and
+    silu(gate) * up runs in fc1's epilogue, so the [S, 2*ffn] output never goes to
+    memory. The LoRA slots of the reference are not part of this path."""
+
+    def __init__(self, fc1, fc2):
+        self.fc1, self.fc2 = fc1, fc2
+        self._tw_pairs = None
+
+    @classmethod
+    def load(cls, weights, prefix, hidden_size, ffn_hidden, dtype=torch.bfloat16):
+        """`H3Transformer.swift:612-616`: fc1 / fc2 MfLinear under prefix.fc1 / prefix.fc2."""
+        return cls(MfLinear.load(weights, prefix + ".fc1", hidden_size, dtype),
+                   MfLinear.load(weights, prefix + ".fc2", ffn_hidden, dtype))
+
+    def _pairs(self):
+        f = self.fc1
+        if (self._tw_pairs is None and f.is_quantized and f.tiled and f.out_dim % 2 == 0 and
+                ops.tiled_supported(f.in_dim, f.group_size, f.bits, f.scales.dtype)):
+            self._tw_pairs = ops.tile(f.w, f.scales, f.biases, f.group_size, f.bits,
+                                      swiglu=True)
+        return self._tw_pairs
+
+    def forward(self, x):
+        tw = self._pairs()
+        if tw is not None:
+            gated = ops.tiled_matmul(x.to(torch.bfloat16).contiguous(), tw, bias=self.fc1.bias,
+                                     activation="swiglu")
+        else:
+            y = self.fc1.forward(x)
+            half = y.shape[-1] // 2
+            gated = (torch.nn.functional.silu(y[..., :half].float()) *
+                     y[..., half:].float()).to(y.dtype)
+        return self.fc2.forward(gated)
+
+    __call__ = forward

@@ -199,11 +199,13 @@ class TiledWeight:
     buffer) plus its geometry. Built once by `tile()`; read by `tiled_matmul`.
     Holds the same bits as the MLX triple, so results are identical."""
 
-    __slots__ = ("data", "N", "K", "group_size", "bits")
+    __slots__ = ("data", "N", "K", "group_size", "bits", "swiglu")
 
-    def __init__(self, data, N, K, group_size, bits):
+    def __init__(self, data, N, K, group_size, bits, swiglu=False):
         self.data, self.N, self.K = data, int(N), int(K)
         self.group_size, self.bits = int(group_size), int(bits)
+        # rows [gate; up] tiled in pairs (mxq_tile_swiglu): only activation="swiglu"
+        self.swiglu = bool(swiglu)
 
     @property
     def device(self):
@@ -220,8 +222,11 @@ def tiled_supported(K, group_size, bits, scales_dtype=torch.bfloat16):
             group_size in _SUPPORTED_GS and scales_dtype == torch.bfloat16)
 
 
-def tile(w, scales, biases, group_size=64, bits=4):
-    """MLX-layout triple -> TiledWeight (one device pass, no requantization)."""
+def tile(w, scales, biases, group_size=64, bits=4, *, swiglu=False):
+    """MLX-layout triple -> TiledWeight (one device pass, no requantization).
+
+    swiglu=True: the weight's rows are [gate; up] (a fused fc1, N even) and are
+    tiled in pairs for tiled_matmul(..., activation="swiglu")."""
     _check_bits_gs("tile", bits, group_size)
     w = _as_words(w)
     _on_gpu("tile", w, scales, biases)
@@ -241,18 +246,32 @@ def tile(w, scales, biases, group_size=64, bits=4):
         _lib.check(int(nbytes))
     w, scales, biases = _dense(w), _dense(scales), _dense(biases)
     data = torch.empty(int(nbytes), dtype=torch.uint8, device=w.device)
-    _lib.check(L.mxq_tile(_ptr(w), _ptr(scales), _ptr(biases), N, K, group_size, bits,
-                          _ptr(data), _stream(w)))
-    return TiledWeight(data, N, K, group_size, bits)
+    fn = L.mxq_tile_swiglu if swiglu else L.mxq_tile
+    _lib.check(fn(_ptr(w), _ptr(scales), _ptr(biases), N, K, group_size, bits, _ptr(data),
+                  _stream(w)))
+    return TiledWeight(data, N, K, group_size, bits, swiglu)
 
 
-def tiled_matmul(x, tw, *, bias=None, path="auto"):
+_ACTIVATIONS = {None: _lib.MXQ_ACT_NONE, "gelu_tanh": _lib.MXQ_ACT_GELU_TANH,
+                "swiglu": _lib.MXQ_ACT_SWIGLU}
+
+
+def tiled_matmul(x, tw, *, bias=None, path="auto", activation=None):
     """quantized_matmul(x, w, scales, biases, transpose=True, ...) on a TiledWeight.
 
-    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv"."""
+    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv".
+    activation (fused into the MFMA kernel's epilogue, applied in fp32 before the
+    one bf16 rounding; any M): None, "gelu_tanh" (geluApprox between the LTX
+    feed-forward projections), or "swiglu" (silu(gate) * up of a weight tiled
+    with swiglu=True; the output has N/2 columns)."""
     op = "quantized_matmul"
     if not isinstance(tw, TiledWeight):
         raise ValueError(f"[{op}] expected a TiledWeight (got {type(tw).__name__}).")
+    if activation not in _ACTIVATIONS:
+        raise ValueError(f"[{op}] unknown activation {activation!r}.")
+    if (activation == "swiglu") != tw.swiglu:
+        raise ValueError(f"[{op}] activation='swiglu' needs, and only accepts, a weight tiled "
+                         f"with swiglu=True.")
     _on_gpu(op, x, tw.data, bias)
     if x.shape[-1] != tw.K:
         raise ValueError(f"[{op}] x.shape[-1] == {x.shape[-1]} does not match the weight's "
@@ -263,12 +282,21 @@ def tiled_matmul(x, tw, *, bias=None, path="auto"):
         raise ValueError(f"[{op}] bias must be bfloat16 of shape ({tw.N},).")
     x, bias = _dense(x), _dense(bias)
     M = x.numel() // tw.K
-    y = torch.empty(tuple(x.shape[:-1]) + (tw.N,), dtype=torch.bfloat16, device=x.device)
+    n_out = tw.N // 2 if activation == "swiglu" else tw.N
+    y = torch.empty(tuple(x.shape[:-1]) + (n_out,), dtype=torch.bfloat16, device=x.device)
+    L = _lib.lib()
+    if activation is not None:
+        if path == "qmv":
+            raise ValueError(f"[{op}] fused activations run on the MFMA kernel (path 'qmm').")
+        _lib.check(L.mxq_qmm_tiled_act(_ptr(x), M, tw.K, _ptr(tw.data), tw.N, tw.group_size,
+                                       tw.bits, _ptr(bias), _ACTIVATIONS[activation], _ptr(y),
+                                       _stream(x)))
+        return y
     fns = {"auto": "mxq_quantized_matmul_tiled", "qmm": "mxq_qmm_tiled",
            "qmv": "mxq_qmv_tiled"}
     if path not in fns:
         raise ValueError(f"unknown path {path!r}")
-    fn = getattr(_lib.lib(), fns[path])
+    fn = getattr(L, fns[path])
     _lib.check(fn(_ptr(x), M, tw.K, _ptr(tw.data), tw.N, tw.group_size, tw.bits, _ptr(bias),
                   _ptr(y), _stream(x)))
     return y
