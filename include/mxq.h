@@ -20,6 +20,11 @@
  *   mxq_pack, mxq_unpack  <- the packed-code layout itself (no MLX-Swift
  *                            function; the layout of `weight` in the triple
  *                            `model/minimax h3/H3Common.swift:280-281, 389-394`)
+ *   mxq_qmm_tiled_act     <- geluApprox(proj_in(x)) of the LTX feed-forward and
+ *                            silu(gate) * up of the H3 MLP, fused into the
+ *                            matmul's epilogue
+ *                            `model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:392-401`,
+ *                            `model/minimax h3/H3Transformer.swift:620-629`
  *
  * Conventions (mirroring mlx-c: int status, out-parameters, no exceptions):
  *   - Every function returns MXQ_OK (0) or a negative MXQ_ERR_* code; the
