@@ -215,6 +215,40 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
     results.update(out)
 
 
+def loader_leg(torch, mx, dev, mb=256):
+    """Host -> HBM upload of a safetensors file of packed weights through libmxq's reader
+    (mmap, two pinned staging buffers, hipMemcpyAsync), page cache warm, against the
+    safetensors package's own load_file(device=...)."""
+    import tempfile
+    from safetensors.torch import load_file, save_file
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "w.safetensors")
+        n = mb * (1 << 20) // 4 // 4
+        g = torch.Generator().manual_seed(0)
+        tensors = {f"l{i}.weight": torch.randint(0, 2 ** 31 - 1, (n,), generator=g,
+                                                 dtype=torch.int32).view(torch.uint32)
+                   for i in range(4)}
+        save_file(tensors, path)
+        nbytes = sum(t.numel() * 4 for t in tensors.values())
+        best = {}
+        for name in ("mxq", "pkg", "mxq", "pkg"):   # first pass of each warms the page cache
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            if name == "mxq":
+                with mx.SafetensorsFile(path, device=dev) as f:
+                    out = [f.get_uncached(k) for k in tensors]
+                    torch.cuda.synchronize()
+            else:
+                out = list(load_file(path, device=str(dev)).values())
+                torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best[name] = min(best.get(name, 1e9), dt)
+            del out
+    return {"bytes": nbytes, "gbs": nbytes / best["mxq"] / 1e9,
+            "gbs_safetensors_pkg": nbytes / best["pkg"] / 1e9,
+            "note": "4 x 64 MiB U32 tensors, page cache warm; open + read + synchronize"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +366,12 @@ def main():
     res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation",
                              **fused}
     del tw_pairs, y_half
+
+    # ---------------- safetensors loader (warm page cache) ----------------
+    res["loader"] = loader_leg(torch, mx, dev)
+    print(f"[bench] loader: {res['loader']['gbs']:.1f} GB/s "
+          f"(safetensors package: {res['loader']['gbs_safetensors_pkg']:.1f} GB/s)",
+          file=sys.stderr, flush=True)
 
     # ---------------- gemv ----------------
     g = GEMV

@@ -182,6 +182,35 @@ int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, in
                       int group_size, int bits, const void* bias, int act, void* y,
                       mxq_stream stream);
 
+/* ---- safetensors files (read-only) -----------------------------------------
+ * The on-disk form of the quantized triples: `prefix.weight` U32 packed codes
+ * plus `prefix.scales` / `prefix.biases` (or `prefix.weight.scales` /
+ * `.weight.biases`), as the reference's H3Weights reads them: header parsed
+ * once, tensors read on demand (`model/minimax h3/H3Common.swift:181-260`),
+ * file mapped read-only (`model/3模块/Safetensors-mmap映射-通用.swift:40-135`).
+ * A handle is not thread-safe. */
+#define MXQ_ST_MAX_DIMS 8
+typedef struct mxq_safetensors mxq_safetensors;
+
+/* Maps `path` and parses its header; MXQ_ERR_INVALID for a missing file or a
+ * malformed header (sizes and ranges are checked against the file). */
+int mxq_st_open(const char* path, mxq_safetensors** out);
+/* Waits for the handle's pending copies, then unmaps and frees it. */
+void mxq_st_close(mxq_safetensors* st);
+/* Number of tensors and the i-th key (header order). */
+int64_t mxq_st_count(const mxq_safetensors* st);
+const char* mxq_st_key(const mxq_safetensors* st, int64_t i);
+/* dtype name ("U32", "BF16", ...), rank, shape and byte size of `key`. */
+int mxq_st_info(const mxq_safetensors* st, const char* key, char dtype[16], int* ndim,
+                int64_t shape[MXQ_ST_MAX_DIMS], int64_t* nbytes);
+/* Copies the tensor's bytes to host memory. */
+int mxq_st_read_host(const mxq_safetensors* st, const char* key, void* dst);
+/* Enqueues the tensor's bytes to device memory `dst` on `stream`: the mapped
+ * bytes are staged through two pinned host buffers (held by the handle, freed
+ * at close), so reading chunk i+1 from the file overlaps the copy of chunk i.
+ * Returns once every chunk is staged; the file may then be closed. */
+int mxq_st_read(mxq_safetensors* st, const char* key, void* dst, mxq_stream stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* mxq_last_error(void);
 

@@ -4,13 +4,15 @@ The quantized-linear hot path of the reference's MLX-Swift DiT backbones,
 rebuilt in HIP for gfx950 behind the same operator surface:
 
     quantized, dequantized, quantized_matmul (quantizedMatmul / quantizedMM),
-    QuantizedLinear, MfLinear
+    QuantizedLinear, MfLinear, the fused feed-forward blocks LTXFFN and H3MlpW,
+    and SafetensorsFile (the on-disk triples, read straight into HBM)
 
 Device memory and streams come from torch; every kernel lives in libmxq.so,
 whose C ABI is include/mxq.h.
 """
 from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
 from .nn import H3MlpW, LTXFFN, MfLinear, QuantizedLinear  # noqa: F401
+from .stfile import SafetensorsFile  # noqa: F401
 from .ops import (TiledWeight, dequantized, pack, quantized, quantized_matmul,  # noqa: F401
                   quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
@@ -18,6 +20,6 @@ from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F
 __all__ = [
     "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
     "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight",
-    "QuantizedLinear", "MfLinear", "get_quantized", "infer_geometry",
-    "header_candidates", "lib", "LIB_PATH", "MXQError",
+    "QuantizedLinear", "MfLinear", "LTXFFN", "H3MlpW", "SafetensorsFile", "get_quantized",
+    "infer_geometry", "header_candidates", "lib", "LIB_PATH", "MXQError",
 ]

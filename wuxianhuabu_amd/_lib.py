@@ -40,6 +40,14 @@ SIGNATURES = {
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),
     "mxq_tile": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
     "mxq_tile_swiglu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
+    "mxq_st_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mxq_st_close": (None, [_vp]),
+    "mxq_st_count": (_i64, [_vp]),
+    "mxq_st_key": (ctypes.c_char_p, [_vp, _i64]),
+    "mxq_st_info": (_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_int), _vp,
+                           ctypes.POINTER(_i64)]),
+    "mxq_st_read_host": (_int, [_vp, ctypes.c_char_p, _vp]),
+    "mxq_st_read": (_int, [_vp, ctypes.c_char_p, _vp, _vp]),
     "mxq_quantized_matmul_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp,
                                           _vp]),
     "mxq_qmm_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),

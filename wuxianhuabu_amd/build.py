@@ -17,7 +17,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmxq.so")
 
-SOURCES = ["mxq_layout.hip", "mxq_qmv.hip", "mxq_qmm.hip", "mxq_qmm_tiled.hip", "mxq_api.cpp"]
+SOURCES = ["mxq_layout.hip", "mxq_qmv.hip", "mxq_qmm.hip", "mxq_qmm_tiled.hip", "mxq_api.cpp",
+           "mxq_safetensors.cpp"]
 HEADERS = ["mxq_device.hpp", "mxq_internal.hpp", "mxq_ring.hpp", "mxq_tiled.hpp"]
 
 ARCH = "gfx950"

@@ -66,6 +66,22 @@ int hip_status(const char* op, hipError_t e) {
   return fail(MXQ_ERR_HIP, "[%s] HIP error: %s", op, hipGetErrorString(e));
 }
 
+}  // namespace
+
+// the thread-local error text, shared with mxq_safetensors.cpp
+namespace mxq {
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+int clear_error() { return ok(); }
+}  // namespace mxq
+
+namespace {
+
 bool dtype_ok(int d) { return d == MXQ_FLOAT32 || d == MXQ_BFLOAT16; }
 
 int check_matmul(const char* op, const void* x, int64_t M, int64_t K, const uint32_t* wq,
