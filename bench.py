@@ -363,7 +363,32 @@ def main():
                        "fused_tflops": flop / (af * 1e-3) / 1e12}
         print(f"[bench] {name}: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
               flush=True)
-    res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation",
+    # LoRA rank 64 (`H3Common.swift:369-375`): fused = xa = x A (torch GEMM) + the qmm with
+    # the rank-64 update in its accumulators; unfused = qmm, then (x A) B with torch, then add
+    gl = torch.Generator(device=dev)
+    gl.manual_seed(77)
+    lora = mx.LoraAdapters([((torch.randn(c["K"], 64, generator=gl, device=dev) * 0.02).bfloat16(),
+                             (torch.randn(64, c["N"], generator=gl, device=dev) * 0.02).bfloat16(),
+                             1.0)])
+
+    def lora_fused(_i):
+        xa = lora.xa(x)
+        ok(L.mxq_qmm_tiled_lora(P(x), c["M"], c["K"], P(tw.data), c["N"], c["gs"], c["bits"],
+                                None, 0, P(xa), P(lora.bt), lora.R, P(y), cur()))
+
+    def lora_unfused(_i):
+        qmm_launch(_i)
+        y.add_(torch.matmul(lora.xa(x), lora.bt.t()))
+
+    pf, _ = time_launches(torch, lora_fused, fused_steps, 2)
+    pu, _ = time_launches(torch, lora_unfused, fused_steps, 2)
+    af, au = sum(pf) / len(pf), sum(pu) / len(pu)
+    fused["lora_rank64"] = {"fused_ms": af, "unfused_ms": au,
+                            "fused_tflops": flop / (af * 1e-3) / 1e12}
+    print(f"[bench] lora r64: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
+          flush=True)
+    del lora
+    res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation / LoRA",
                              **fused}
     del tw_pairs, y_half
 

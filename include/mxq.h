@@ -22,7 +22,8 @@
  *                            `model/minimax h3/H3Common.swift:280-281, 389-394`)
  *   mxq_qmm_tiled_act     <- geluApprox(proj_in(x)) of the LTX feed-forward and
  *                            silu(gate) * up of the H3 MLP, fused into the
- *                            matmul's epilogue
+ *                            matmul's epilogue (mxq_qmm_tiled_lora: plus the
+ *                            LoRA term, `model/minimax h3/H3Common.swift:369-375`)
  *                            `model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:392-401`,
  *                            `model/minimax h3/H3Transformer.swift:620-629`
  *
@@ -181,6 +182,18 @@ int mxq_tile_swiglu(const uint32_t* wq, const void* scales, const void* biases, 
 int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
                       int group_size, int bits, const void* bias, int act, void* y,
                       mxq_stream stream);
+
+/* mxq_qmm_tiled_act plus a rank-R update added to the fp32 accumulators before the
+ * bias, the activation and the rounding: y = act(x*W^T + bias + xa*bt^T). This is
+ * the LoRA term of the reference's MfLinear.forward, out + sum_i scale_i (x A_i) B_i
+ * (`model/minimax h3/H3Common.swift:369-375, 421-434`): xa bf16 [M, R] = x [A_1 | A_2
+ * | ...] (the caller's small GEMM), bt bf16 [N, R] = [scale_1 B_1; scale_2 B_2; ...]^T,
+ * rows in the weight's row order ([gate; up] for MXQ_ACT_SWIGLU). R a positive
+ * multiple of 16 (zero-pad the adapters), at most 4096. xa == bt == NULL, R == 0:
+ * no update. */
+int mxq_qmm_tiled_lora(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                       int group_size, int bits, const void* bias, int act, const void* xa,
+                       const void* bt, int64_t R, void* y, mxq_stream stream);
 
 /* ---- safetensors files (read-only) -----------------------------------------
  * The on-disk form of the quantized triples: `prefix.weight` U32 packed codes

@@ -13,13 +13,14 @@ whose C ABI is include/mxq.h.
 from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
 from .nn import H3MlpW, LTXFFN, MfLinear, QuantizedLinear  # noqa: F401
 from .stfile import SafetensorsFile  # noqa: F401
-from .ops import (TiledWeight, dequantized, pack, quantized, quantized_matmul,  # noqa: F401
+from .ops import (LoraAdapters, TiledWeight, dequantized, pack, quantized,  # noqa: F401
+                  quantized_matmul,
                   quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
 
 __all__ = [
     "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
-    "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight",
+    "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight", "LoraAdapters",
     "QuantizedLinear", "MfLinear", "LTXFFN", "H3MlpW", "SafetensorsFile", "get_quantized",
     "infer_geometry", "header_candidates", "lib", "LIB_PATH", "MXQError",
 ]

@@ -52,6 +52,8 @@ SIGNATURES = {
                                           _vp]),
     "mxq_qmm_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_qmm_tiled_act": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _int, _vp, _vp]),
+    "mxq_qmm_tiled_lora": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _int, _vp, _vp,
+                                  _i64, _vp, _vp]),
     "mxq_qmv_tiled": (_int, [_vp, _i64, _i64, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_last_error": (ctypes.c_char_p, []),
     "mxq_status_string": (ctypes.c_char_p, [_int]),

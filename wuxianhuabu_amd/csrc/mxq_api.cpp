@@ -324,9 +324,9 @@ int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void*
 }
 }  // namespace
 
-int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
-                      int group_size, int bits, const void* bias, int act, void* y,
-                      mxq_stream stream) {
+int mxq_qmm_tiled_lora(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                       int group_size, int bits, const void* bias, int act, const void* xa,
+                       const void* bt, int64_t R, void* y, mxq_stream stream) {
   int rc = check_tiled("quantized_matmul", x, M, K, tiled, N, group_size, bits, bias, y);
   if (rc) return rc;
   if (act != MXQ_ACT_NONE && act != MXQ_ACT_GELU_TANH && act != MXQ_ACT_SWIGLU)
@@ -335,13 +335,36 @@ int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, in
     return fail(MXQ_ERR_INVALID,
                 "[quantized_matmul] SwiGLU needs an even number of weight rows (got %lld).",
                 static_cast<long long>(N));
+  if (xa || bt || R) {
+    if (R <= 0 || R % 16 != 0 || R > 4096)
+      return fail(MXQ_ERR_INVALID,
+                  "[quantized_matmul] The low-rank update needs a rank R that is a positive "
+                  "multiple of 16, at most 4096 (got %lld).",
+                  static_cast<long long>(R));
+    if (M * R * 2 > INT32_MAX || N * R * 2 > INT32_MAX)
+      return fail(MXQ_ERR_INVALID, "[quantized_matmul] xa or bt above 2^31-1 bytes.");
+    if (M > 0 && N > 0) {
+      if (!xa || !bt) return fail(MXQ_ERR_NULL, "[quantized_matmul] xa and bt must be non-NULL.");
+      if (!aligned4(xa) || !aligned4(bt))
+        return fail(MXQ_ERR_ALIGNMENT, "[quantized_matmul] xa and bt must be 4-byte aligned.");
+    }
+  }
   if (M == 0 || N == 0) return ok();
   return hip_status("quantized_matmul",
                     mxq::detail::launch_qmm_tiled(
                         static_cast<const uint16_t*>(x), static_cast<int>(M),
                         static_cast<int>(K), tiled, static_cast<int>(N), group_size, bits,
-                        static_cast<const uint16_t*>(bias), act, static_cast<uint16_t*>(y),
+                        static_cast<const uint16_t*>(bias), act,
+                        static_cast<const uint16_t*>(xa), static_cast<const uint16_t*>(bt),
+                        static_cast<int>(R), static_cast<uint16_t*>(y),
                         static_cast<hipStream_t>(stream)));
+}
+
+int mxq_qmm_tiled_act(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,
+                      int group_size, int bits, const void* bias, int act, void* y,
+                      mxq_stream stream) {
+  return mxq_qmm_tiled_lora(x, M, K, tiled, N, group_size, bits, bias, act, nullptr, nullptr,
+                            0, y, stream);
 }
 
 int mxq_qmm_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_t N,

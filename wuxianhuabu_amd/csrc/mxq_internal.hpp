@@ -42,10 +42,11 @@ bool qmm_supports_bits(int bits);
 
 // Both kernels on tiled weights (K % 64 == 0): any M for the MFMA kernel,
 // M <= 8 for the GEMV.
-// act: MXQ_ACT_* (mxq.h), applied in the MFMA kernel's epilogue.
+// act: MXQ_ACT_* (mxq.h), applied in the MFMA kernel's epilogue; xa [M, R] and
+// bt [N, R] (bf16, R % 16 == 0; xa == nullptr for none) add xa . bt^T first.
 hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
-                            int bits, const uint16_t* bias, int act, uint16_t* y,
-                            hipStream_t s);
+                            int bits, const uint16_t* bias, int act, const uint16_t* xa,
+                            const uint16_t* bt, int R, uint16_t* y, hipStream_t s);
 hipError_t launch_qmv_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
                             int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
 

@@ -126,6 +126,7 @@ class MfLinear:
         self.group_size = 0
         self.tiled = True
         self._tw = None
+        self.lora = None  # LoraAdapters (set_lora), the reference's LoraSlot
 
     @classmethod
     def load(cls, weights, prefix, in_features, dtype=torch.bfloat16):
@@ -154,24 +155,42 @@ class MfLinear:
             lin.bias = b.to(dtype).contiguous()
         return lin
 
+    def set_lora(self, refs):
+        """Attach LoRA adapters [(a [in, r], b [r, out], scale), ...]
+        (`H3Common.swift:405-434`); an empty list detaches them."""
+        refs = list(refs)
+        self.lora = ops.LoraAdapters(refs) if refs else None
+        return self
+
+    def tiled_weight(self):
+        if self._tw is None and self.is_quantized and self.tiled and ops.tiled_supported(
+                self.in_dim, self.group_size, self.bits, self.scales.dtype):
+            self._tw = ops.tile(self.w, self.scales, self.biases, self.group_size, self.bits)
+        return self._tw
+
     def forward(self, x):
+        """`H3Common.swift:341-377`: bf16 quantized matmul, + bias, + the LoRA term. On
+        tiled weights the LoRA term joins the fp32 accumulators in the kernel, before
+        the bias and the one rounding."""
         if self.is_quantized:
             if self.scales.dtype != torch.bfloat16:
                 raise ValueError("MfLinear: the quantized kernels take bfloat16 scales/biases")
             xc = x.to(torch.bfloat16).contiguous()
-            if self._tw is None and self.tiled and ops.tiled_supported(
-                    self.in_dim, self.group_size, self.bits, self.scales.dtype):
-                self._tw = ops.tile(self.w, self.scales, self.biases, self.group_size,
-                                    self.bits)
-            if self._tw is not None:
-                return ops.tiled_matmul(xc, self._tw, bias=self.bias)
-            return ops.quantized_matmul(xc, self.w, self.scales, self.biases, transpose=True,
-                                        group_size=self.group_size, bits=self.bits,
-                                        bias=self.bias)
-        # dense branch: not part of the quantized path; plain device matmul
-        out = x.to(self.w.dtype) @ self.w
-        if self.bias is not None:
-            out = out + self.bias
+            tw = self.tiled_weight()
+            if tw is not None:
+                return ops.tiled_matmul(xc, tw, bias=self.bias, lora=self.lora)
+            out = ops.quantized_matmul(xc, self.w, self.scales, self.biases, transpose=True,
+                                       group_size=self.group_size, bits=self.bits,
+                                       bias=self.bias)
+        else:
+            # dense branch: not part of the quantized path; plain device matmul
+            xc = x.to(self.w.dtype)
+            out = xc @ self.w
+            if self.bias is not None:
+                out = out + self.bias
+        if self.lora is not None:
+            xa = self.lora.xa(xc.reshape(-1, self.in_dim).to(torch.bfloat16))
+            out = out + (xa.float() @ self.lora.bt.float().t()).to(out.dtype).reshape(out.shape)
         return out
 
     __call__ = forward
@@ -209,7 +228,8 @@ class H3MlpW:
     [S, 2*ffn] (gate and up fused), silu(gate) * up, fc2. When fc1 is quantized and
     tileable its weight is tiled once in gate/up pairs (mxq_tile_swiglu) and
     silu(gate) * up runs in fc1's epilogue, so the [S, 2*ffn] output never goes to
-    memory. The LoRA slots of the reference are not part of this path."""
+    memory. fc1's LoRA adapters (MfLinear.set_lora, the reference's fc1Lora) join the
+    accumulators before it."""
 
     def __init__(self, fc1, fc2):
         self.fc1, self.fc2 = fc1, fc2
@@ -233,7 +253,7 @@ class H3MlpW:
         tw = self._pairs()
         if tw is not None:
             gated = ops.tiled_matmul(x.to(torch.bfloat16).contiguous(), tw, bias=self.fc1.bias,
-                                     activation="swiglu")
+                                     activation="swiglu", lora=self.fc1.lora)
         else:
             y = self.fc1.forward(x)
             half = y.shape[-1] // 2

@@ -256,14 +256,57 @@ _ACTIVATIONS = {None: _lib.MXQ_ACT_NONE, "gelu_tanh": _lib.MXQ_ACT_GELU_TANH,
                 "swiglu": _lib.MXQ_ACT_SWIGLU}
 
 
-def tiled_matmul(x, tw, *, bias=None, path="auto", activation=None):
+class LoraAdapters:
+    """LoRA adapters of one linear layer, prepared for the fused kernel: the
+    reference's LoraSlot of LoraRef(a [in, r], b [r, out], scale)
+    (`model/minimax h3/H3Common.swift:405-434`), whose term is
+    sum_i scale_i * (x a_i) b_i. Held as a_cat [in, R] = [a_1 | a_2 | ...] and
+    bt [out, R] = [scale_1 b_1; scale_2 b_2; ...]^T in bf16, R padded with zeros
+    to a multiple of 16."""
+
+    __slots__ = ("a_cat", "bt", "R", "rank")
+
+    def __init__(self, refs):
+        refs = list(refs)
+        if not refs:
+            raise ValueError("[lora] no adapters given.")
+        a0, b0, _ = refs[0]
+        din, dout = int(a0.shape[0]), int(b0.shape[1])
+        for a, b, _ in refs:
+            if a.ndim != 2 or b.ndim != 2 or a.shape[0] != din or b.shape[1] != dout or \
+                    a.shape[1] != b.shape[0]:
+                raise ValueError("[lora] every adapter needs a [in, r] and b [r, out] with the "
+                                 "same in and out.")
+        self.rank = sum(int(a.shape[1]) for a, _, _ in refs)
+        self.R = (self.rank + 15) // 16 * 16
+        if self.R > 4096:
+            raise ValueError(f"[lora] total rank {self.rank} above 4096.")
+        dev = a0.device
+        a_cat = torch.zeros(din, self.R, dtype=torch.bfloat16, device=dev)
+        bt = torch.zeros(dout, self.R, dtype=torch.bfloat16, device=dev)
+        o = 0
+        for a, b, scale in refs:
+            r = int(a.shape[1])
+            a_cat[:, o:o + r] = a.to(torch.bfloat16)
+            bt[:, o:o + r] = (b.float() * float(scale)).t().to(torch.bfloat16)
+            o += r
+        self.a_cat, self.bt = a_cat, bt
+
+    def xa(self, x2d):
+        """x [M, in] bf16 -> x a_cat [M, R] bf16 (a plain library GEMM)."""
+        return torch.matmul(x2d, self.a_cat).contiguous()
+
+
+def tiled_matmul(x, tw, *, bias=None, path="auto", activation=None, lora=None):
     """quantized_matmul(x, w, scales, biases, transpose=True, ...) on a TiledWeight.
 
     path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv".
     activation (fused into the MFMA kernel's epilogue, applied in fp32 before the
     one bf16 rounding; any M): None, "gelu_tanh" (geluApprox between the LTX
     feed-forward projections), or "swiglu" (silu(gate) * up of a weight tiled
-    with swiglu=True; the output has N/2 columns)."""
+    with swiglu=True; the output has N/2 columns).
+    lora: LoraAdapters whose term is added to the MFMA kernel's accumulators
+    before the bias, the activation and the rounding (any M)."""
     op = "quantized_matmul"
     if not isinstance(tw, TiledWeight):
         raise ValueError(f"[{op}] expected a TiledWeight (got {type(tw).__name__}).")
@@ -285,12 +328,21 @@ def tiled_matmul(x, tw, *, bias=None, path="auto", activation=None):
     n_out = tw.N // 2 if activation == "swiglu" else tw.N
     y = torch.empty(tuple(x.shape[:-1]) + (n_out,), dtype=torch.bfloat16, device=x.device)
     L = _lib.lib()
-    if activation is not None:
+    if activation is not None or lora is not None:
         if path == "qmv":
-            raise ValueError(f"[{op}] fused activations run on the MFMA kernel (path 'qmm').")
-        _lib.check(L.mxq_qmm_tiled_act(_ptr(x), M, tw.K, _ptr(tw.data), tw.N, tw.group_size,
-                                       tw.bits, _ptr(bias), _ACTIVATIONS[activation], _ptr(y),
-                                       _stream(x)))
+            raise ValueError(f"[{op}] fused activations and LoRA run on the MFMA kernel "
+                             f"(path 'qmm').")
+        xa = bt = None
+        R = 0
+        if lora is not None:
+            if not isinstance(lora, LoraAdapters):
+                raise ValueError(f"[{op}] lora must be LoraAdapters.")
+            if tuple(lora.a_cat.shape) != (tw.K, lora.R) or tuple(lora.bt.shape) != (tw.N, lora.R):
+                raise ValueError(f"[{op}] LoRA shapes do not match the weight [{tw.N}, {tw.K}].")
+            xa, bt, R = lora.xa(x.reshape(M, tw.K)), lora.bt, lora.R
+        _lib.check(L.mxq_qmm_tiled_lora(_ptr(x), M, tw.K, _ptr(tw.data), tw.N, tw.group_size,
+                                        tw.bits, _ptr(bias), _ACTIVATIONS[activation],
+                                        _ptr(xa), _ptr(bt), R, _ptr(y), _stream(x)))
         return y
     fns = {"auto": "mxq_quantized_matmul_tiled", "qmm": "mxq_qmm_tiled",
            "qmv": "mxq_qmv_tiled"}
