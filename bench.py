@@ -215,6 +215,57 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
     results.update(out)
 
 
+def blockops_leg(torch, mx, dev, steps, S=14400, hidden=5376, H=42, hd=128, rot=96):
+    """The H3 block's row ops at the 720p token count (hidden 5376; q/k of 42 heads x 128,
+    rotary on 96 dims): GB/s of algorithmic bytes (rows read and written once), against
+    torch's unfused chain of the reference's fallback path."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    bf = torch.bfloat16
+    x = torch.randn(S, hidden, generator=g, device=dev).to(bf)
+    other = torch.randn(S, hidden, generator=g, device=dev).to(bf)
+    w = torch.randn(hidden, generator=g, device=dev).to(bf)
+    mods = torch.randn(3, 3, hidden, generator=g, device=dev).to(bf)
+    rmap = mx.build_row_mod_map(S, [(0, S // 2, 1), (S // 2, S, 2)], device=dev)
+    q = torch.randn(1, S, H, hd, generator=g, device=dev).to(bf)
+    qw = torch.randn(hd, generator=g, device=dev).to(bf)
+    th = torch.rand(S, rot // 2, generator=g, device=dev) * 6.28
+    cos, sin = th.cos(), th.sin()
+    idx = rmap.view(torch.int32).long()
+
+    def rms(t, wt):
+        tf = t.float()
+        return (tf * torch.rsqrt(tf.square().mean(-1, keepdim=True) + 1e-6) * wt.float()).to(bf)
+
+    def rope_unfused():
+        n = rms(q, qw)
+        x1, x2, tail = n[..., :rot // 2], n[..., rot // 2:rot], n[..., rot:]
+        c, sn = cos.view(1, S, 1, -1), sin.view(1, S, 1, -1)
+        return torch.cat([x1 * c - x2 * sn, x2 * c + x1 * sn, tail], -1)
+
+    cases = {
+        "norm_modscale": (lambda: mx.fused_norm_modscale(x, w, mods[0], mods[1], rmap, 1e-6),
+                          lambda: rms(x, w) * (mods[1][idx] + 1) + mods[0][idx],
+                          2 * S * hidden * 2),
+        "mod_gate": (lambda: mx.fused_mod_gate(x, mods[2], other, rmap),
+                     lambda: x + other * mods[2][idx], 3 * S * hidden * 2),
+        "rmsnorm_rope": (lambda: mx.fused_rmsnorm_rope(q, qw, cos, sin, rot, 1e-6),
+                         rope_unfused, 2 * S * H * hd * 2 + 2 * S * (rot // 2) * 4),
+    }
+    out = {"shape": {"S": S, "hidden": hidden, "heads": H, "head_dim": hd, "rot": rot}}
+    n = max(10, steps)
+    for name, (fused, unfused, nbytes) in cases.items():
+        pf, _ = time_launches(torch, lambda _i: fused(), n, 3)
+        pu, _ = time_launches(torch, lambda _i: unfused(), max(5, n // 3), 2)
+        af, au = sum(pf) / len(pf), sum(pu) / len(pu)
+        out[name] = {"us": af * 1e3, "gbs": nbytes / (af * 1e-3) / 1e9,
+                     "frac_hbm": nbytes / (af * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "unfused_us": au * 1e3, "bytes": nbytes}
+        print(f"[bench] {name}: {af * 1e3:.1f} us ({out[name]['gbs']:.0f} GB/s), "
+              f"torch unfused {au * 1e3:.1f} us", file=sys.stderr, flush=True)
+    return out
+
+
 def loader_leg(torch, mx, dev, mb=256):
     """Host -> HBM upload of a safetensors file of packed weights through libmxq's reader
     (mmap, two pinned staging buffers, hipMemcpyAsync), page cache warm, against the
@@ -391,6 +442,9 @@ def main():
     res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation / LoRA",
                              **fused}
     del tw_pairs, y_half
+
+    # ---------------- H3 block row ops (HBM-bound) ----------------
+    res["blockops"] = blockops_leg(torch, mx, dev, steps)
 
     # ---------------- safetensors loader (warm page cache) ----------------
     res["loader"] = loader_leg(torch, mx, dev)

@@ -195,6 +195,35 @@ int mxq_qmm_tiled_lora(const void* x, int64_t M, int64_t K, const void* tiled, i
                        int group_size, int bits, const void* bias, int act, const void* xa,
                        const void* bt, int64_t R, void* y, mxq_stream stream);
 
+/* ---- row-wise ops of the DiT block around the linears -----------------------
+ * The H3 block's fused kernels (`model/2网络算子/网络算子-融合-RMSNormRoPE-通用.swift:41-343`,
+ * called at `model/minimax h3/H3Transformer.swift:455-480, 1117-1155`), with their
+ * arithmetic: fp32 mean of squares, rsqrt, the normalised value rounded to bf16,
+ * then the modulation or rotation in fp32 and one more bf16 rounding. x, other,
+ * weight, shift, scale, gate and out are bf16; row_map [S] picks the modulation
+ * row of each token row (NULL: row 0; entries past mod_rows - 1 are clamped).
+ * HBM-bound; one wave per row. */
+
+/* out [S, hidden] = (rmsnorm(x) * weight) * (scale[m] + 1) + shift[m]:
+ * rmsNormLast + modScaleShift (fusedNormModscale / fusedNormModscaleRow);
+ * shift, scale [mod_rows, hidden]. */
+int mxq_norm_modscale(const void* x, int64_t S, int64_t hidden, const void* weight,
+                      const void* shift, const void* scale, int64_t mod_rows,
+                      const uint32_t* row_map, float eps, void* out, mxq_stream stream);
+
+/* out [S, hidden] = x + other * gate[m] (fusedModGate); gate [mod_rows, hidden]. */
+int mxq_mod_gate(const void* x, const void* other, int64_t S, int64_t hidden, const void* gate,
+                 int64_t mod_rows, const uint32_t* row_map, void* out, mxq_stream stream);
+
+/* out [S, heads, head_dim] = split-half rotary of rmsnorm(x) * weight over the last axis
+ * (fusedRmsnormRope = rmsNormLast + applyRopePub, `H3Common.swift:502-508, 555-569`): for
+ * j < rot/2, (n_j, n_{j+rot/2}) rotate by the angle of (token, j); dims >= rot pass
+ * through. weight [head_dim]; cos, sin [S, rot/2] in table_dtype (MXQ_FLOAT32 or
+ * MXQ_BFLOAT16). head_dim <= 512, rot even, rot <= head_dim. */
+int mxq_rmsnorm_rope(const void* x, int64_t S, int64_t heads, int64_t head_dim,
+                     const void* weight, const void* cos, const void* sin, int table_dtype,
+                     int rot, float eps, void* out, mxq_stream stream);
+
 /* ---- safetensors files (read-only) -----------------------------------------
  * The on-disk form of the quantized triples: `prefix.weight` U32 packed codes
  * plus `prefix.scales` / `prefix.biases` (or `prefix.weight.scales` /

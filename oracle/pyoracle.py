@@ -276,3 +276,49 @@ def tile_swiglu(wq, scales, biases, K, gs, bits):
     rows = swiglu_rows(wq.shape[0])
     pick = lambda a: np.where((rows >= 0)[:, None], a[np.maximum(rows, 0)], 0).astype(a.dtype)
     return tile(pick(wq), pick(scales), pick(biases), K, gs, bits)
+
+
+# ---------------------------------------------------------------- H3 block row ops
+def _f32_of(u16):
+    return bf16_to_f32(np.asarray(u16, np.uint16))
+
+
+def rmsnorm_bf16(x, w, eps):
+    """rmsNormLast as the fused kernels evaluate it (`model/minimax h3/H3Common.swift:502-508`;
+    `网络算子-融合-RMSNormRoPE-通用.swift:52-82`): fp32 mean of squares, rsqrt, x * rstd * w
+    in fp32, rounded to bf16. x, w bf16 bits; returns float32 values of the bf16 result."""
+    xf = _f32_of(x)
+    wf = _f32_of(w)
+    var = (xf.astype(np.float64) ** 2).mean(axis=-1, keepdims=True)
+    rstd = (1.0 / np.sqrt(var + eps)).astype(np.float32)
+    return bf16_to_f32(bf16_rne((xf * rstd) * wf))
+
+
+def norm_modscale_f64(x, w, shift, scale, row_map, eps):
+    """fusedNormModscale before its last rounding (`网络算子-融合-RMSNormRoPE-通用.swift:132-167`):
+    n * (scale[m] + 1) + shift[m] with n = rmsnorm_bf16."""
+    n = rmsnorm_bf16(x, w, eps).astype(np.float64)
+    m = np.zeros(n.shape[0], np.int64) if row_map is None else np.asarray(row_map, np.int64)
+    return n * (_f32_of(scale)[m].astype(np.float64) + 1.0) + _f32_of(shift)[m]
+
+
+def mod_gate_f64(x, other, gate, row_map):
+    """fusedModGate before its rounding (:177-199): x + other * gate[m]."""
+    m = np.zeros(np.asarray(x).shape[0], np.int64) if row_map is None else \
+        np.asarray(row_map, np.int64)
+    return _f32_of(x).astype(np.float64) + _f32_of(other).astype(np.float64) * _f32_of(gate)[m]
+
+
+def rmsnorm_rope_f64(x, w, cos, sin, rot, eps):
+    """fusedRmsnormRope before its last rounding (:41-110; applyRopePub, `H3Common.swift:555-569`):
+    x [S, H, hd] bf16 bits, cos / sin [S, rot/2] float; pairs (j, j + rot/2) rotate, the tail
+    passes through."""
+    n = rmsnorm_bf16(x, w, eps).astype(np.float64)
+    rh = rot // 2
+    out = n.copy()
+    c = np.asarray(cos, np.float64)[:, None, :]
+    s = np.asarray(sin, np.float64)[:, None, :]
+    x1, x2 = n[..., :rh], n[..., rh:rot]
+    out[..., :rh] = x1 * c - x2 * s
+    out[..., rh:rot] = x2 * c + x1 * s
+    return out

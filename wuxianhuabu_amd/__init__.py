@@ -13,6 +13,8 @@ whose C ABI is include/mxq.h.
 from ._lib import LIB_PATH, MXQError, lib  # noqa: F401
 from .nn import H3MlpW, LTXFFN, MfLinear, QuantizedLinear  # noqa: F401
 from .stfile import SafetensorsFile  # noqa: F401
+from .blockops import (build_row_mod_map, fused_mod_gate, fused_norm_modscale,  # noqa: F401
+                       fused_norm_modscale_row, fused_rmsnorm_rope)
 from .ops import (LoraAdapters, TiledWeight, dequantized, pack, quantized,  # noqa: F401
                   quantized_matmul,
                   quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
@@ -23,4 +25,6 @@ __all__ = [
     "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight", "LoraAdapters",
     "QuantizedLinear", "MfLinear", "LTXFFN", "H3MlpW", "SafetensorsFile", "get_quantized",
     "infer_geometry", "header_candidates", "lib", "LIB_PATH", "MXQError",
+    "fused_norm_modscale", "fused_norm_modscale_row", "fused_mod_gate", "fused_rmsnorm_rope",
+    "build_row_mod_map",
 ]

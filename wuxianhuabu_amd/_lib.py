@@ -40,6 +40,11 @@ SIGNATURES = {
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),
     "mxq_tile": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
     "mxq_tile_swiglu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
+    "mxq_norm_modscale": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, ctypes.c_float,
+                                 _vp, _vp]),
+    "mxq_mod_gate": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "mxq_rmsnorm_rope": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _int, _int,
+                                ctypes.c_float, _vp, _vp]),
     "mxq_st_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mxq_st_close": (None, [_vp]),
     "mxq_st_count": (_i64, [_vp]),

@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 
 #include "mxq_internal.hpp"
 #include "mxq_tiled.hpp"
@@ -411,3 +412,81 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
 }
 
 }  // extern "C"
+
+// ---- row-wise ops of the DiT block (mxq_blockops.hip)
+
+namespace {
+bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+
+int check_rows(const char* op, int64_t S, int64_t hidden,
+               std::initializer_list<const void*> required) {
+  if (S < 0 || hidden < 0) return fail(MXQ_ERR_INVALID, "[%s] Negative dimension.", op);
+  if (hidden > INT32_MAX) return fail(MXQ_ERR_INVALID, "[%s] Row above 2^31-1 elements.", op);
+  if (S == 0 || hidden == 0) return MXQ_OK;
+  for (const void* p : required) {
+    if (!p) return fail(MXQ_ERR_NULL, "[%s] A required tensor pointer is NULL.", op);
+    if (!aligned2(p)) return fail(MXQ_ERR_ALIGNMENT, "[%s] bf16 tensors must be 2-byte aligned.", op);
+  }
+  return MXQ_OK;
+}
+}  // namespace
+
+int mxq_norm_modscale(const void* x, int64_t S, int64_t hidden, const void* weight,
+                      const void* shift, const void* scale, int64_t mod_rows,
+                      const uint32_t* row_map, float eps, void* out, mxq_stream stream) {
+  int rc = check_rows("norm_modscale", S, hidden, {x, weight, shift, scale, out});
+  if (rc) return rc;
+  if (S > 0 && hidden > 0 && mod_rows < 1)
+    return fail(MXQ_ERR_INVALID, "[norm_modscale] mod_rows must be at least 1.");
+  if (row_map && !aligned4(row_map))
+    return fail(MXQ_ERR_ALIGNMENT, "[norm_modscale] row_map must be 4-byte aligned.");
+  return hip_status("norm_modscale",
+                    mxq::detail::launch_norm_modscale(
+                        static_cast<const uint16_t*>(x), S, static_cast<int>(hidden),
+                        static_cast<const uint16_t*>(weight), static_cast<const uint16_t*>(shift),
+                        static_cast<const uint16_t*>(scale), row_map, mod_rows, eps,
+                        static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream)));
+}
+
+int mxq_mod_gate(const void* x, const void* other, int64_t S, int64_t hidden, const void* gate,
+                 int64_t mod_rows, const uint32_t* row_map, void* out, mxq_stream stream) {
+  int rc = check_rows("mod_gate", S, hidden, {x, other, gate, out});
+  if (rc) return rc;
+  if (S > 0 && hidden > 0 && mod_rows < 1)
+    return fail(MXQ_ERR_INVALID, "[mod_gate] mod_rows must be at least 1.");
+  if (row_map && !aligned4(row_map))
+    return fail(MXQ_ERR_ALIGNMENT, "[mod_gate] row_map must be 4-byte aligned.");
+  return hip_status("mod_gate", mxq::detail::launch_mod_gate(
+                                    static_cast<const uint16_t*>(x),
+                                    static_cast<const uint16_t*>(other), S,
+                                    static_cast<int>(hidden), static_cast<const uint16_t*>(gate),
+                                    row_map, mod_rows, static_cast<uint16_t*>(out),
+                                    static_cast<hipStream_t>(stream)));
+}
+
+int mxq_rmsnorm_rope(const void* x, int64_t S, int64_t heads, int64_t head_dim,
+                     const void* weight, const void* cos, const void* sin, int table_dtype,
+                     int rot, float eps, void* out, mxq_stream stream) {
+  if (heads < 0) return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] Negative dimension.");
+  int rc = check_rows("rmsnorm_rope", S * heads, head_dim, {x, weight, out});
+  if (rc) return rc;
+  if (head_dim > 512)
+    return fail(MXQ_ERR_UNSUPPORTED, "[rmsnorm_rope] head_dim %lld above 512.",
+                static_cast<long long>(head_dim));
+  if (rot < 0 || rot % 2 || rot > head_dim)
+    return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] rot must be even and at most head_dim (got %d).",
+                rot);
+  if (table_dtype != MXQ_FLOAT32 && table_dtype != MXQ_BFLOAT16)
+    return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] Unknown table dtype %d.", table_dtype);
+  if (S * heads > 0 && head_dim > 0 && rot > 0 && (!cos || !sin))
+    return fail(MXQ_ERR_NULL, "[rmsnorm_rope] cos and sin must be non-NULL.");
+  if ((cos && !aligned2(cos)) || (sin && !aligned2(sin)) ||
+      (table_dtype == MXQ_FLOAT32 && ((cos && !aligned4(cos)) || (sin && !aligned4(sin)))))
+    return fail(MXQ_ERR_ALIGNMENT, "[rmsnorm_rope] cos and sin must be aligned to their dtype.");
+  return hip_status("rmsnorm_rope",
+                    mxq::detail::launch_rmsnorm_rope(
+                        static_cast<const uint16_t*>(x), S, static_cast<int>(heads),
+                        static_cast<int>(head_dim), static_cast<const uint16_t*>(weight), cos, sin,
+                        table_dtype, rot, eps, static_cast<uint16_t*>(out),
+                        static_cast<hipStream_t>(stream)));
+}

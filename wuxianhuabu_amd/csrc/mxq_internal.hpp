@@ -50,5 +50,17 @@ hipError_t launch_qmm_tiled(const uint16_t* x, int M, int K, const void* tiled, 
 hipError_t launch_qmv_tiled(const uint16_t* x, int M, int K, const void* tiled, int N, int gs,
                             int bits, const uint16_t* bias, uint16_t* y, hipStream_t s);
 
+// Row-wise ops of the DiT block around the linears (mxq_blockops.hip): bf16 rows.
+hipError_t launch_norm_modscale(const uint16_t* x, int64_t S, int hidden, const uint16_t* w,
+                                const uint16_t* shift, const uint16_t* scale,
+                                const uint32_t* map, int64_t mod_rows, float eps, uint16_t* out,
+                                hipStream_t s);
+hipError_t launch_mod_gate(const uint16_t* x, const uint16_t* other, int64_t S, int hidden,
+                           const uint16_t* gate, const uint32_t* map, int64_t mod_rows,
+                           uint16_t* out, hipStream_t s);
+hipError_t launch_rmsnorm_rope(const uint16_t* x, int64_t S, int H, int hd, const uint16_t* w,
+                               const void* c, const void* sn, int table_dtype, int rot,
+                               float eps, uint16_t* out, hipStream_t s);
+
 }  // namespace detail
 }  // namespace mxq
