@@ -382,21 +382,34 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     for (int nb = 0; nb < 2; ++nb)
       bo[nb] = ((glu ? (nb ? N / 2 : 0) + c0 : c0 + nb * 32) + l32) * rank * 2 + g2 * 16;
     const int ao = l32 * rank * 2 + g2 * 16;
-    for (int c = 0; c < rank; c += 16) {
-      bf16x8 bw[2];
+    // chunk c + 16's operands are requested before chunk c's MFMAs (the last chunk is
+    // requested twice: harmless), so each wait covers one chunk of MFMAs less latency
+    bf16x8 bw[2], av[MB];
+    auto fetch = [&](int c, bf16x8 (&b)[2], bf16x8 (&a)[MB]) __attribute__((always_inline)) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
-        bw[nb] = __builtin_bit_cast(
+        b[nb] = __builtin_bit_cast(
             bf16x8, __builtin_amdgcn_raw_buffer_load_b128(br, bo[nb] + c * 2, 0, 0));
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const bf16x8 av = __builtin_bit_cast(
+      for (int mb = 0; mb < MB; ++mb)
+        a[mb] = __builtin_bit_cast(
             bf16x8,
             __builtin_amdgcn_raw_buffer_load_b128(ar, ao + c * 2 + mb * 32 * rank * 2, 0, 0));
+    };
+    fetch(0, bw, av);
+    for (int c = 0; c < rank; c += 16) {
+      bf16x8 bn[2], an[MB];
+      fetch(min(c + 16, rank - 16), bn, an);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
-          acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[nb], av, acc[nb][mb], 0, 0, 0);
-      }
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[nb], av[mb], acc[nb][mb], 0,
+                                                                0, 0);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) bw[nb] = bn[nb];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) av[mb] = an[mb];
     }
   };
 
