@@ -308,6 +308,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip oracle check and CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--all", action="store_true", help="also time c0, c1, c3-down, c4 chain")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the tiled qmm and GEMV (what the rocprof summaries trace)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a plain elementwise copy of 1 GiB -> 1 GiB three times "
                          "(the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -365,12 +367,13 @@ def main():
         ok(L.mxq_qmm(P(x), c["M"], c["K"], P(wq), P(s), P(b), c["N"], c["gs"], c["bits"], None,
                      P(y), cur()))
 
-    torch.cuda.synchronize()
-    mper, _ = time_launches(torch, qmm_mlx_launch, max(5, steps // 3), 2)
-    mavg = sum(mper) / len(mper)
-    res["qmm_mlx_layout"] = {"kernel_avg_ms": mavg,
-                             "tflops": 2.0 * c["M"] * c["N"] * c["K"] / (mavg * 1e-3) / 1e12}
-    print(f"[bench] qmm (MLX layout): avg {mavg:.3f} ms", file=sys.stderr, flush=True)
+    if not args.headline_only:
+        torch.cuda.synchronize()
+        mper, _ = time_launches(torch, qmm_mlx_launch, max(5, steps // 3), 2)
+        mavg = sum(mper) / len(mper)
+        res["qmm_mlx_layout"] = {"kernel_avg_ms": mavg,
+                                 "tflops": 2.0 * c["M"] * c["N"] * c["K"] / (mavg * 1e-3) / 1e12}
+        print(f"[bench] qmm (MLX layout): avg {mavg:.3f} ms", file=sys.stderr, flush=True)
     per, total = time_launches(torch, qmm_launch, steps, warmup)
     flop = 2.0 * c["M"] * c["N"] * c["K"]
     per_sorted = sorted(per)
@@ -381,76 +384,77 @@ def main():
     print(f"[bench] qmm: avg {avg_ms:.3f} ms  median {med_ms:.3f} ms  "
           f"{achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
-    # ---------------- fused epilogues on the same workload ----------------
-    # GELU-tanh (LTX feed-forward) and silu(gate) * up (H3 MLP, the weight's rows read as
-    # [gate; up] and tiled in pairs) in the qmm's epilogue, against the unfused chain:
-    # the same qmm writing bf16, then torch's elementwise activation on it.
-    fused_steps = max(5, steps // 3)
-    tw_pairs = mx.tile(wq, s, b, c["gs"], c["bits"], swiglu=True)
-    half = c["N"] // 2
-    y_half = torch.empty(c["M"], half, dtype=torch.bfloat16, device=dev)
+    if not args.headline_only:
+        # ---------------- fused epilogues on the same workload ----------------
+        # GELU-tanh (LTX feed-forward) and silu(gate) * up (H3 MLP, the weight's rows read as
+        # [gate; up] and tiled in pairs) in the qmm's epilogue, against the unfused chain:
+        # the same qmm writing bf16, then torch's elementwise activation on it.
+        fused_steps = max(5, steps // 3)
+        tw_pairs = mx.tile(wq, s, b, c["gs"], c["bits"], swiglu=True)
+        half = c["N"] // 2
+        y_half = torch.empty(c["M"], half, dtype=torch.bfloat16, device=dev)
 
-    def fused_launch(act, t, out):
-        def f(_i):
-            ok(L.mxq_qmm_tiled_act(P(x), c["M"], c["K"], P(t.data), c["N"], c["gs"],
-                                   c["bits"], None, act, P(out), cur()))
-        return f
+        def fused_launch(act, t, out):
+            def f(_i):
+                ok(L.mxq_qmm_tiled_act(P(x), c["M"], c["K"], P(t.data), c["N"], c["gs"],
+                                       c["bits"], None, act, P(out), cur()))
+            return f
 
-    def gelu_unfused(_i):
-        qmm_launch(_i)
-        torch.nn.functional.gelu(y, approximate="tanh")
+        def gelu_unfused(_i):
+            qmm_launch(_i)
+            torch.nn.functional.gelu(y, approximate="tanh")
 
-    def swiglu_unfused(_i):
-        qmm_launch(_i)
-        torch.mul(torch.nn.functional.silu(y[:, :half]), y[:, half:], out=y_half)
+        def swiglu_unfused(_i):
+            qmm_launch(_i)
+            torch.mul(torch.nn.functional.silu(y[:, :half]), y[:, half:], out=y_half)
 
-    fused = {}
-    for name, fn_f, fn_u in (("gelu_tanh", fused_launch(1, tw, y), gelu_unfused),
-                             ("swiglu", fused_launch(2, tw_pairs, y_half), swiglu_unfused)):
-        pf, _ = time_launches(torch, fn_f, fused_steps, 2)
-        pu, _ = time_launches(torch, fn_u, fused_steps, 2)
+        fused = {}
+        for name, fn_f, fn_u in (("gelu_tanh", fused_launch(1, tw, y), gelu_unfused),
+                                 ("swiglu", fused_launch(2, tw_pairs, y_half), swiglu_unfused)):
+            pf, _ = time_launches(torch, fn_f, fused_steps, 2)
+            pu, _ = time_launches(torch, fn_u, fused_steps, 2)
+            af, au = sum(pf) / len(pf), sum(pu) / len(pu)
+            fused[name] = {"fused_ms": af, "unfused_ms": au,
+                           "fused_tflops": flop / (af * 1e-3) / 1e12}
+            print(f"[bench] {name}: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
+                  flush=True)
+        # LoRA rank 64 (`H3Common.swift:369-375`): fused = xa = x A (torch GEMM) + the qmm with
+        # the rank-64 update in its accumulators; unfused = qmm, then (x A) B with torch, then add
+        gl = torch.Generator(device=dev)
+        gl.manual_seed(77)
+        lora = mx.LoraAdapters([((torch.randn(c["K"], 64, generator=gl, device=dev) * 0.02).bfloat16(),
+                                 (torch.randn(64, c["N"], generator=gl, device=dev) * 0.02).bfloat16(),
+                                 1.0)])
+
+        def lora_fused(_i):
+            xa = lora.xa(x)
+            ok(L.mxq_qmm_tiled_lora(P(x), c["M"], c["K"], P(tw.data), c["N"], c["gs"], c["bits"],
+                                    None, 0, P(xa), P(lora.bt), lora.R, P(y), cur()))
+
+        def lora_unfused(_i):
+            qmm_launch(_i)
+            y.add_(torch.matmul(lora.xa(x), lora.bt.t()))
+
+        pf, _ = time_launches(torch, lora_fused, fused_steps, 2)
+        pu, _ = time_launches(torch, lora_unfused, fused_steps, 2)
         af, au = sum(pf) / len(pf), sum(pu) / len(pu)
-        fused[name] = {"fused_ms": af, "unfused_ms": au,
-                       "fused_tflops": flop / (af * 1e-3) / 1e12}
-        print(f"[bench] {name}: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
+        fused["lora_rank64"] = {"fused_ms": af, "unfused_ms": au,
+                                "fused_tflops": flop / (af * 1e-3) / 1e12}
+        print(f"[bench] lora r64: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
               flush=True)
-    # LoRA rank 64 (`H3Common.swift:369-375`): fused = xa = x A (torch GEMM) + the qmm with
-    # the rank-64 update in its accumulators; unfused = qmm, then (x A) B with torch, then add
-    gl = torch.Generator(device=dev)
-    gl.manual_seed(77)
-    lora = mx.LoraAdapters([((torch.randn(c["K"], 64, generator=gl, device=dev) * 0.02).bfloat16(),
-                             (torch.randn(64, c["N"], generator=gl, device=dev) * 0.02).bfloat16(),
-                             1.0)])
+        del lora
+        res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation / LoRA",
+                                 **fused}
+        del tw_pairs, y_half
 
-    def lora_fused(_i):
-        xa = lora.xa(x)
-        ok(L.mxq_qmm_tiled_lora(P(x), c["M"], c["K"], P(tw.data), c["N"], c["gs"], c["bits"],
-                                None, 0, P(xa), P(lora.bt), lora.R, P(y), cur()))
+        # ---------------- H3 block row ops (HBM-bound) ----------------
+        res["blockops"] = blockops_leg(torch, mx, dev, steps)
 
-    def lora_unfused(_i):
-        qmm_launch(_i)
-        y.add_(torch.matmul(lora.xa(x), lora.bt.t()))
-
-    pf, _ = time_launches(torch, lora_fused, fused_steps, 2)
-    pu, _ = time_launches(torch, lora_unfused, fused_steps, 2)
-    af, au = sum(pf) / len(pf), sum(pu) / len(pu)
-    fused["lora_rank64"] = {"fused_ms": af, "unfused_ms": au,
-                            "fused_tflops": flop / (af * 1e-3) / 1e12}
-    print(f"[bench] lora r64: fused {af:.3f} ms, unfused {au:.3f} ms", file=sys.stderr,
-          flush=True)
-    del lora
-    res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation / LoRA",
-                             **fused}
-    del tw_pairs, y_half
-
-    # ---------------- H3 block row ops (HBM-bound) ----------------
-    res["blockops"] = blockops_leg(torch, mx, dev, steps)
-
-    # ---------------- safetensors loader (warm page cache) ----------------
-    res["loader"] = loader_leg(torch, mx, dev)
-    print(f"[bench] loader: {res['loader']['gbs']:.1f} GB/s "
-          f"(safetensors package: {res['loader']['gbs_safetensors_pkg']:.1f} GB/s)",
-          file=sys.stderr, flush=True)
+        # ---------------- safetensors loader (warm page cache) ----------------
+        res["loader"] = loader_leg(torch, mx, dev)
+        print(f"[bench] loader: {res['loader']['gbs']:.1f} GB/s "
+              f"(safetensors package: {res['loader']['gbs_safetensors_pkg']:.1f} GB/s)",
+              file=sys.stderr, flush=True)
 
     # ---------------- gemv ----------------
     g = GEMV
@@ -473,10 +477,11 @@ def main():
     # 100 launches per graph (20 passes over the 5 copies), replayed `steps` times
     glaunch = 20 * g["copies"]
     greplays = max(steps, 5)
-    mper, _ = time_graph(torch, gemv_mlx_launch, glaunch, greplays, rotate=g["copies"])
-    mavg = sum(mper) / len(mper)
-    res["gemv_mlx_layout"] = {"us_per_launch": mavg * 1e3,
-                              "gbs": gemv_bytes(g) / (mavg * 1e-3) / 1e9}
+    if not args.headline_only:
+        mper, _ = time_graph(torch, gemv_mlx_launch, glaunch, greplays, rotate=g["copies"])
+        mavg = sum(mper) / len(mper)
+        res["gemv_mlx_layout"] = {"us_per_launch": mavg * 1e3,
+                                  "gbs": gemv_bytes(g) / (mavg * 1e-3) / 1e9}
     gper, gtotal = time_graph(torch, gemv_launch, glaunch, greplays, rotate=g["copies"])
     gsteps = glaunch * greplays
     gbytes = gemv_bytes(g)
