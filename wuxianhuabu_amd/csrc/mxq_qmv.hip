@@ -15,6 +15,8 @@
 // Per 16-code chunk the affine form is factored:
 //   sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k
 // so each weight costs one decode and MT fused multiply-adds.
+#include <type_traits>
+
 #include "mxq_device.hpp"
 #include "mxq_internal.hpp"
 #include "mxq_ring.hpp"
@@ -230,12 +232,12 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 // bytes in flight with as little VALU work per byte as possible: one
 // workgroup of a few waves per 32-row record half; the waves split the K steps
 // into contiguous spans (a row block's records are contiguous in HBM). Each
-// wave, per batch of up to SPW steps:
-//   1. moves its activation slice (MT rows x SPW steps x 128 B) into its own
-//      LDS region with LDS-direct loads (no other wave reads it: no barrier);
-//   2. issues every weight load of the batch at once;
-//   3. waits for the batch, sums each activation half-run once, and consumes
-//      the records.
+// wave works in batches of up to SPW steps, with two register sets: while
+// batch b computes, every load of batch b+1 (its activation slice, MT rows x
+// SPW steps x 128 B, and its weight units) is in flight. Computing a batch
+// writes its activation slice to the wave's own LDS region (no other wave
+// reads it: no barrier), sums each activation half-run once, and consumes the
+// records.
 // Per step a lane owns one unit (row l32 of the half, code half g2): 32 codes
 // from a coalesced 16-byte plane plus remainder words.
 //
@@ -268,10 +270,10 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   static_assert(MT <= 8, "a lane half holds 4 tokens of the MFMA output");
   constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
   constexpr int RB = tiled::code_bytes(BITS) + 256 * GP;      // record bytes
-  // activation bytes per wave, a whole number of LDS-direct loads (64 lanes x
+  // activation bytes per wave, a whole number of 1 KiB pieces (64 lanes x
   // 16 B each): the padding of small MT x SPW receives repeats of valid rows
   constexpr int XW = (MT * SPW * 128 + 1023) / 1024 * 1024;
-  constexpr int XLOADS = XW / 1024;                           // LDS-direct loads per batch
+  constexpr int XLOADS = XW / 1024;                           // 16-byte loads per lane per batch
   constexpr int NSUM = MT * SPW * 2;                          // half-run sums per batch
   constexpr int RPL = MT < 4 ? MT : 4;                        // tokens per lane half
   static_assert(NH * 32 * MT * 4 <= XW, "partials reuse the activation region");
@@ -327,57 +329,68 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 #pragma unroll
     for (int r = 0; r < RPL; ++r) acc[nb][r] = 0.f;
 
-  for (int b0 = k_begin; b0 < k_end; b0 += SPW) {
-    // 1. activations of steps b0 .. b0+SPW-1 (clamped; rows past M repeat a
-    //    valid row, their sums are never stored): LDS byte o of this wave's
-    //    region holds row o / (SPW*128), step (o / 128) % SPW, 16-byte chunk
-    //    (o / 16) % 8
-    __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  // One batch of loads, into registers (the compiler waits for each register
+  // where it is first used): the activations of steps b0 .. b0+SPW-1 (clamped;
+  // rows past M repeat a valid row, whose sums are never stored), 16 bytes per
+  // lane per 1 KiB piece, and every weight unit of the batch (clamped: repeats
+  // are never used). Piece i, lane byte o = i*1024 + lane*16 holds row
+  // o / (SPW*128), step (o / 128) % SPW, 16-byte chunk (o / 16) % 8.
+  struct Batch {
+    v4u_t x[XLOADS];
+    uint32_t w[SPW][NH][BITS];
+    uint32_t sb[SPW][NH][GP];
+  };
+  auto load = [&](Batch& B, int b0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XLOADS; ++i) {
       const int o = i * 1024 + lane * 16;
       const int m = min(o / (SPW * 128), mcount - 1);
       const int st = min(b0 + (o / 128) % SPW, k_end - 1);
-      ring::lds_load<16>(xrs, xw + i * 1024, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0);
+      B.x[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          xrs, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0, 0);
     }
-    asm volatile("" ::: "memory");  // the activation request stays ahead of the wait below
-    // 2. every weight unit of the batch (clamped: repeats are never used)
-    uint32_t w[SPW][NH][BITS];
-    uint32_t sb[SPW][NH][GP];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const int so = min(b0 + j, k_end - 1) * RB;
+      // uniform, kept in an SGPR (a VGPR soffset would become a readfirstlane loop)
+      const int so = __builtin_amdgcn_readfirstlane(min(b0 + j, k_end - 1) * RB);
 #pragma unroll
       for (int nb = 0; nb < NH; ++nb) {
 #pragma unroll
         for (int p = 0; p < FP; ++p) {
           const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
-          w[j][nb][4 * p] = v.x; w[j][nb][4 * p + 1] = v.y;
-          w[j][nb][4 * p + 2] = v.z; w[j][nb][4 * p + 3] = v.w;
+          B.w[j][nb][4 * p] = v.x; B.w[j][nb][4 * p + 1] = v.y;
+          B.w[j][nb][4 * p + 2] = v.z; B.w[j][nb][4 * p + 3] = v.w;
         }
         if constexpr (RW == 1) {
-          w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+          B.w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
         } else if constexpr (RW == 2) {
           const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
-          w[j][nb][4 * FP] = v.x; w[j][nb][4 * FP + 1] = v.y;
+          B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
         } else if constexpr (RW == 3) {
           const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
-          w[j][nb][4 * FP] = v.x; w[j][nb][4 * FP + 1] = v.y; w[j][nb][4 * FP + 2] = v.z;
+          B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
+          B.w[j][nb][4 * FP + 2] = v.z;
         }
         if constexpr (GP == 2) {
           const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, svo[nb], so, 0);
-          sb[j][nb][0] = v.x;
-          sb[j][nb][GP - 1] = v.y;
+          B.sb[j][nb][0] = v.x;
+          B.sb[j][nb][GP - 1] = v.y;
         } else {
-          sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+          B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
         }
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // 3. everything of the batch has landed (correct whatever order the loads
-    //    were issued in); half-run sums: item t = (m, step, half) is the sum of
-    //    its four 16-byte chunks, one chunk per lane, met by two lane swaps
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  // The batch's arithmetic: the activations go to this wave's LDS region (LDS
+  // operations of one wave run in order, so the previous batch's reads of it
+  // are done first), then half-run sums: item t = (m, step, half) is the sum
+  // of its four 16-byte chunks, one chunk per lane, met by two lane swaps.
+  // FULLB: all SPW steps lie before k_end (true of every batch but a wave's last)
+  auto consume = [&](auto fullc, const Batch& B, int b0) __attribute__((always_inline)) {
+    constexpr bool FULLB = decltype(fullc)::value;
+#pragma unroll
+    for (int i = 0; i < XLOADS; ++i)
+      *reinterpret_cast<v4u_t*>(xw + i * 1024 + lane * 16) = B.x[i];
 #pragma unroll
     for (int t0 = 0; t0 < NSUM * 4; t0 += 64) {
       const int u = t0 + lane;                 // (item, chunk) = (u / 4, u % 4)
@@ -394,7 +407,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     __builtin_amdgcn_s_waitcnt((15 & 15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      if (b0 + j >= k_end) break;
+      if (!FULLB && b0 + j >= k_end) break;
       // step sums of this lane's tokens 4*g2 + r (zero past MT), per group
       float xs[GP][RPL];
 #pragma unroll
@@ -424,10 +437,10 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           for (int i = 0; i < 4; ++i) {
             const int q = 8 * c + 2 * i;
             if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
-              pr[i] = pack_bf16x2(static_cast<float>(code_at<BITS>(w[j][nb], q)),
-                                  static_cast<float>(code_at<BITS>(w[j][nb], q + 1)));
+              pr[i] = pack_bf16x2(static_cast<float>(code_at<BITS>(B.w[j][nb], q)),
+                                  static_cast<float>(code_at<BITS>(B.w[j][nb], q + 1)));
             else
-              pr[i] = pair_at<BITS>(w[j][nb], q, kPairMask, kMagic);
+              pr[i] = pair_at<BITS>(B.w[j][nb], q, kPairMask, kMagic);
           }
           bv[c] = __builtin_bit_cast(bf16x8, v4u_t{pr[0], pr[1], pr[2], pr[3]});
         }
@@ -438,14 +451,42 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           for (int c = 0; c < 4; ++c)
             d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[e][c], bv[c], c == 0 ? f32x16_t{} : d,
                                                         0, 0, 0);
-          const float sc = __uint_as_float(sb[j][nb][e] << 16);
-          const float bi = __uint_as_float(sb[j][nb][e] & 0xFFFF0000u);
+          const float sc = __uint_as_float(B.sb[j][nb][e] << 16);
+          const float bi = __uint_as_float(B.sb[j][nb][e] & 0xFFFF0000u);
           const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
 #pragma unroll
           for (int r = 0; r < RPL; ++r)
             acc[nb][r] = fmaf(sc, d[r], fmaf(b2, xs[e][r], acc[nb][r]));
         }
       }
+    }
+  };
+  // two register sets: batch b+1's loads are in flight while batch b computes.
+  // Each consume follows its prefetch (or the absence of one) in straight-line
+  // code, and a batch with a prefetch behind it is whole (no early exit that
+  // would leave its loads unwaited), so the compiler's wait before the batch's
+  // first use counts the prefetch as still in flight instead of waiting for it.
+  using Whole = std::true_type;
+  using Part = std::false_type;
+  Batch ba, bb;
+  int b0 = k_begin;
+  if (b0 < k_end) {
+    load(ba, b0);
+    for (;;) {
+      if (b0 + SPW >= k_end) {
+        consume(Part{}, ba, b0);
+        break;
+      }
+      load(bb, b0 + SPW);
+      consume(Whole{}, ba, b0);
+      b0 += SPW;
+      if (b0 + SPW >= k_end) {
+        consume(Part{}, bb, b0);
+        break;
+      }
+      load(ba, b0 + SPW);
+      consume(Whole{}, bb, b0);
+      b0 += SPW;
     }
   }
 
@@ -474,10 +515,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   }
 }
 
-// Launch shape (measured best at M = 1, 2 and 8 for K = 4096, N = 24576 among
-// 1-2 halves x 2-16 waves x 2-16 steps): one workgroup per 32-row record half
-// (768 workgroups at N = 24576, three per CU), 4 waves, batches of 4 steps.
-constexpr int kTiledNH = 1, kTiledWaves = 4, kTiledSPW = 4;
+// Launch shape (measured at M = 1, 2 and 8 for K = 4096, N = 24576 among 2-8
+// waves x 1-8 steps per batch, with the two register sets): one workgroup per
+// 32-row record half (768 workgroups at N = 24576, three per CU), 4 waves,
+// batches of 2 steps.
+constexpr int kTiledNH = 1, kTiledWaves = 4, kTiledSPW = 2;
 
 template <int BITS, int MT>
 hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
