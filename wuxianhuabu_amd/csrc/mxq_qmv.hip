@@ -335,19 +335,35 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // lane per 1 KiB piece, and every weight unit of the batch (clamped: repeats
   // are never used). Piece i, lane byte o = i*1024 + lane*16 holds row
   // o / (SPW*128), step (o / 128) % SPW, 16-byte chunk (o / 16) % 8.
+  // lane part of the activation offsets of a whole batch (row, step within the
+  // batch, chunk); the batch's first step comes in as the scalar offset
+  int xvo[XLOADS];
+#pragma unroll
+  for (int i = 0; i < XLOADS; ++i) {
+    const int o = i * 1024 + lane * 16;
+    xvo[i] = (min(o / (SPW * 128), mcount - 1) * K + ((o / 128) % SPW) * 64) * 2 +
+             ((o / 16) % 8) * 16;
+  }
   struct Batch {
     v4u_t x[XLOADS];
     uint32_t w[SPW][NH][BITS];
     uint32_t sb[SPW][NH][GP];
   };
   auto load = [&](Batch& B, int b0) __attribute__((always_inline)) {
+    if (b0 + SPW <= k_end) {  // whole batch: the step offset is uniform (soffset)
 #pragma unroll
-    for (int i = 0; i < XLOADS; ++i) {
-      const int o = i * 1024 + lane * 16;
-      const int m = min(o / (SPW * 128), mcount - 1);
-      const int st = min(b0 + (o / 128) % SPW, k_end - 1);
-      B.x[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          xrs, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0, 0);
+      for (int i = 0; i < XLOADS; ++i)
+        B.x[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            xrs, xvo[i], __builtin_amdgcn_readfirstlane(b0 * 128), 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < XLOADS; ++i) {
+        const int o = i * 1024 + lane * 16;
+        const int m = min(o / (SPW * 128), mcount - 1);
+        const int st = min(b0 + (o / 128) % SPW, k_end - 1);
+        B.x[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            xrs, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0, 0);
+      }
     }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
