@@ -160,11 +160,16 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
         "cosine": float((yg.ravel() @ ref.ravel()) /
                         (np.linalg.norm(yg) * np.linalg.norm(ref))),
     }
+    out["qmm_check"]["pass"] = out["qmm_check"]["max_rel_vs_exact"] <= 2e-2
     gx, gwq, gs_, gb, gy = bufs["gemv"]
     gref = O.qmm_f64(host_u16(gx), host_u32(gwq), host_u16(gs_), host_u16(gb), gemv_c["gs"],
                      gemv_c["bits"], threads=threads)
     gyh = gy.float().cpu().numpy().astype(np.float64)
-    out["gemv_check"] = {"max_rel_vs_exact": float(np.abs(gyh - gref).max() / np.abs(gref).max())}
+    gemv_rel = float(np.abs(gyh - gref).max() / np.abs(gref).max())
+    out["gemv_check"] = {"max_rel_vs_exact": gemv_rel, "pass": gemv_rel <= 2e-2}
+    for k in ("qmm_check", "gemv_check"):
+        if not out[k]["pass"]:
+            print(f"[bench] {k} FAILED: {out[k]}", file=sys.stderr, flush=True)
 
     # -- CPU baseline: mlx CPU qmm loop structure, bf16 arithmetic, 1 core --
     K, N = qmm_c["K"], qmm_c["N"]
@@ -393,6 +398,8 @@ def main():
         tw_pairs = mx.tile(wq, s, b, c["gs"], c["bits"], swiglu=True)
         half = c["N"] // 2
         y_half = torch.empty(c["M"], half, dtype=torch.bfloat16, device=dev)
+        # the fused legs write their own output, so `y` keeps the plain qmm result
+        y_ep = torch.empty_like(y)
 
         def fused_launch(act, t, out):
             def f(_i):
@@ -401,15 +408,15 @@ def main():
             return f
 
         def gelu_unfused(_i):
-            qmm_launch(_i)
-            torch.nn.functional.gelu(y, approximate="tanh")
+            qmm_launch(_i, y=y_ep)
+            torch.nn.functional.gelu(y_ep, approximate="tanh")
 
         def swiglu_unfused(_i):
-            qmm_launch(_i)
-            torch.mul(torch.nn.functional.silu(y[:, :half]), y[:, half:], out=y_half)
+            qmm_launch(_i, y=y_ep)
+            torch.mul(torch.nn.functional.silu(y_ep[:, :half]), y_ep[:, half:], out=y_half)
 
         fused = {}
-        for name, fn_f, fn_u in (("gelu_tanh", fused_launch(1, tw, y), gelu_unfused),
+        for name, fn_f, fn_u in (("gelu_tanh", fused_launch(1, tw, y_ep), gelu_unfused),
                                  ("swiglu", fused_launch(2, tw_pairs, y_half), swiglu_unfused)):
             pf, _ = time_launches(torch, fn_f, fused_steps, 2)
             pu, _ = time_launches(torch, fn_u, fused_steps, 2)
@@ -429,11 +436,11 @@ def main():
         def lora_fused(_i):
             xa = lora.xa(x)
             ok(L.mxq_qmm_tiled_lora(P(x), c["M"], c["K"], P(tw.data), c["N"], c["gs"], c["bits"],
-                                    None, 0, P(xa), P(lora.bt), lora.R, P(y), cur()))
+                                    None, 0, P(xa), P(lora.bt), lora.R, P(y_ep), cur()))
 
         def lora_unfused(_i):
-            qmm_launch(_i)
-            y.add_(torch.matmul(lora.xa(x), lora.bt.t()))
+            qmm_launch(_i, y=y_ep)
+            y_ep.add_(torch.matmul(lora.xa(x), lora.bt.t()))
 
         pf, _ = time_launches(torch, lora_fused, fused_steps, 2)
         pu, _ = time_launches(torch, lora_unfused, fused_steps, 2)
@@ -445,7 +452,7 @@ def main():
         del lora
         res["fused_epilogue"] = {"workload": "qmm 6-bit M=14400 K=4096 N=16384 + activation / LoRA",
                                  **fused}
-        del tw_pairs, y_half
+        del tw_pairs, y_half, y_ep
 
         # ---------------- H3 block row ops (HBM-bound) ----------------
         res["blockops"] = blockops_leg(torch, mx, dev, steps)
@@ -540,6 +547,8 @@ def main():
 
     # ---------------- CPU leg (oracle) ----------------
     if not args.no_cpu:
+        qmm_launch(0)  # the check reads the plain qmm output of the headline call
+        torch.cuda.synchronize()
         cpu_leg(res, {"qmm": (x, wq, s, b, y), "gemv": (gx, gwq, gs_, gb, gy)}, QMM, GEMV,
                 args.cpu_budget)
 
