@@ -99,6 +99,34 @@ def test_tiled_qmm_several_tiles_per_workgroup(dev, O, bits, gs, K, M, N):
     assert_tight(host_f32_of_bf16(y_t)[rows], ref, f"tiled qmm bits={bits} gs={gs} K={K}")
 
 
+@pytest.mark.parametrize("bits,gs", [(6, 64), (4, 32), (8, 128)])
+def test_tiled_qmm_large_scales(dev, O, bits, gs):
+    """Scales of magnitude 2^104 and above (s * 2^24 overflows fp32) take the
+    kernel's plain unpack for their whole record; records around them keep the
+    fast one. Outputs stay bit-identical to the MLX-layout kernel and within the
+    tight bound of the oracle. Activations are scaled down so y stays finite."""
+    M, N, K = 300, 192, 512
+    rng = np.random.default_rng(bits * 10 + gs)
+    codes = rng.integers(0, 2 ** bits, size=(N, K), dtype=np.uint32)
+    wq = O.pack_words(codes, bits)
+    ng = K // gs
+    e = rng.integers(-8, 9, size=(N, ng))
+    big = rng.random((N, ng)) < 0.1                       # about one group in ten
+    e[big] = rng.integers(104, 118, size=int(big.sum()))
+    sgn = np.where(rng.random((N, ng)) < 0.5, -1.0, 1.0)
+    s = O.bf16_rne((sgn * np.ldexp(1.0 + rng.random((N, ng)), e)).astype(np.float32))
+    b = O.bf16_rne((-0.5 * (2 ** bits) * O.bf16_to_f32(s)).astype(np.float32))
+    x = O.bf16_rne(np.ldexp(rng.standard_normal((M, K)), -118).astype(np.float32))
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y_t = _tiled_run(dev, x, tw, None, path="qmm")
+    y_m = mx.quantized_matmul(dev_bf16(x, dev), dev_words(wq, dev), dev_bf16(s, dev),
+                              dev_bf16(b, dev), group_size=gs, bits=bits, path="qmm")
+    np.testing.assert_array_equal(host_bf16(y_t), host_bf16(y_m))
+    y = host_f32_of_bf16(y_t)
+    assert np.isfinite(y).all()
+    assert_tight(y, O.qmm_f64_bf16w(x, wq, s, b, gs, bits), f"large scales bits={bits} gs={gs}")
+
+
 @pytest.mark.parametrize("M,N,K", [(9, 64, 64), (33, 1, 128), (64, 130, 192), (65, 200, 320),
                                    (129, 63, 256), (257, 300, 512), (1000, 100, 1088)])
 def test_tiled_qmm_shapes(dev, O, M, N, K):
