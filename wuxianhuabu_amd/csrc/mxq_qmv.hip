@@ -263,10 +263,19 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 
 // NH record halves (32 rows each) per workgroup of WPB waves; batches of SPW
 // steps per wave; MT <= 8 tokens.
-template <int BITS, int MT, int GP, int NH, int WPB, int SPW>
+//
+// MLX: the same kernel over the MLX layout itself (wq [N, K*BITS/32], scales and
+// biases [N, K/gs], K % 64 == 0), for callers that keep no tiled copy. Lane
+// (l32, g2) of row block rb, half h, reads the BITS words of codes
+// [64k + 32 g2, +32) of row 64 rb + 32 h + l32 (a run of 32 codes is BITS whole
+// words) and that row's scale and bias of step k's group(s), then everything
+// else is shared. gshift = log2(gs / 64) for gs >= 64.
+template <int BITS, int MT, int GP, int NH, int WPB, int SPW, bool MLX>
 __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
+    const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scs,
+    const uint16_t* __restrict__ bis, int gshift) {
   static_assert(MT <= 8, "a lane half holds 4 tokens of the MFMA output");
   constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
   constexpr int RB = tiled::code_bytes(BITS) + 256 * GP;      // record bytes
@@ -292,17 +301,38 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   uint8_t* const xw = lds + wave * XW;
   float* const xsum = xsum_all[wave];
 
-  const __amdgpu_buffer_rsrc_t wrs = ring::make_rsrc(
-      tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
   const __amdgpu_buffer_rsrc_t xrs = ring::make_rsrc(
       x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(mcount) * K * 2);
+  // weight (and, MLX layout, scale and bias) sources of this workgroup's rows;
+  // the lane parts of the offsets stay in the vector offset, which the buffer
+  // range check covers
+  __amdgpu_buffer_rsrc_t wrs, srs, brs;
   int wvo[NH], rvo[NH], svo[NH];
+  if constexpr (MLX) {
+    const int rowb = K / 8 * BITS;                      // bytes per weight row
+    const int G = GP == 2 ? K >> 5 : K >> (6 + gshift);  // groups per row
+    const int r0 = rb * 64, rows = min(64, N - r0);
+    wrs = ring::make_rsrc(wq + static_cast<int64_t>(r0) * (rowb / 4),
+                          static_cast<uint32_t>(rows) * rowb);
+    srs = ring::make_rsrc(scs + static_cast<int64_t>(r0) * G, static_cast<uint32_t>(rows) * G * 2);
+    brs = ring::make_rsrc(bis + static_cast<int64_t>(r0) * G, static_cast<uint32_t>(rows) * G * 2);
 #pragma unroll
-  for (int nb = 0; nb < NH; ++nb) {
-    const int h = h0 + nb;
-    wvo[nb] = h * tiled::half_bytes(BITS) + lane * 16;
-    rvo[nb] = h * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
-    svo[nb] = tiled::code_bytes(BITS) + (h * 32 + l32) * GP * 4;  // both groups if GP == 2
+    for (int nb = 0; nb < NH; ++nb) {
+      const int r = min((h0 + nb) * 32 + l32, rows - 1);  // rows past N repeat the last one
+      wvo[nb] = r * rowb + g2 * BITS * 4;
+      rvo[nb] = wvo[nb] + FP * 16;
+      svo[nb] = r * G * 2;
+    }
+  } else {
+    wrs = ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
+    srs = brs = wrs;
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) {
+      const int h = h0 + nb;
+      wvo[nb] = h * tiled::half_bytes(BITS) + lane * 16;
+      rvo[nb] = h * tiled::half_bytes(BITS) + FP * 1024 + lane * 4 * RW;
+      svo[nb] = tiled::code_bytes(BITS) + (h * 32 + l32) * GP * 4;  // both groups if GP == 2
+    }
   }
   // A operand rows: token l32 of the batch's activations, zeros past MT. With
   // two groups per step (GP == 2) each code half gets its own MFMA set, whose A
@@ -344,10 +374,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     xvo[i] = (min(o / (SPW * 128), mcount - 1) * K + ((o / 128) % SPW) * 64) * 2 +
              ((o / 16) % 8) * 16;
   }
+  // sb: tiled, the unit's scale (low half) and bias (high half) dword per group;
+  // MLX, sb[..][0] the scale(s) and sb[..][GP - 1] the bias(es) as loaded (GP == 2:
+  // both groups' values in one dword; GP == 1: one value, zero-extended). They
+  // are split where used, so the loads stay in flight until then.
   struct Batch {
     v4u_t x[XLOADS];
     uint32_t w[SPW][NH][BITS];
-    uint32_t sb[SPW][NH][GP];
+    uint32_t sb[SPW][NH][MLX ? 2 : GP];
   };
   auto load = [&](Batch& B, int b0) __attribute__((always_inline)) {
     if (b0 + SPW <= k_end) {  // whole batch: the step offset is uniform (soffset)
@@ -368,12 +402,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       // uniform, kept in an SGPR (a VGPR soffset would become a readfirstlane loop)
-      const int so = __builtin_amdgcn_readfirstlane(min(b0 + j, k_end - 1) * RB);
+      const int kj = min(b0 + j, k_end - 1);
+      const int so = __builtin_amdgcn_readfirstlane(MLX ? kj * 8 * BITS : kj * RB);
 #pragma unroll
       for (int nb = 0; nb < NH; ++nb) {
 #pragma unroll
         for (int p = 0; p < FP; ++p) {
-          const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+          const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * (MLX ? 16 : 1024),
+                                                                so, 0);
           B.w[j][nb][4 * p] = v.x; B.w[j][nb][4 * p + 1] = v.y;
           B.w[j][nb][4 * p + 2] = v.z; B.w[j][nb][4 * p + 3] = v.w;
         }
@@ -387,7 +423,17 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
           B.w[j][nb][4 * FP + 2] = v.z;
         }
-        if constexpr (GP == 2) {
+        if constexpr (MLX) {
+          if constexpr (GP == 2) {  // groups 2k and 2k + 1
+            const int ss = __builtin_amdgcn_readfirstlane(kj * 4);
+            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], ss, 0);
+            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo[nb], ss, 0);
+          } else {                  // group k >> gshift
+            const int ss = __builtin_amdgcn_readfirstlane((kj >> gshift) * 2);
+            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
+            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+          }
+        } else if constexpr (GP == 2) {
           const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, svo[nb], so, 0);
           B.sb[j][nb][0] = v.x;
           B.sb[j][nb][GP - 1] = v.y;
@@ -467,8 +513,15 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           for (int c = 0; c < 4; ++c)
             d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[e][c], bv[c], c == 0 ? f32x16_t{} : d,
                                                         0, 0, 0);
-          const float sc = __uint_as_float(B.sb[j][nb][e] << 16);
-          const float bi = __uint_as_float(B.sb[j][nb][e] & 0xFFFF0000u);
+          float sc, bi;
+          if constexpr (MLX) {
+            const uint32_t sv = B.sb[j][nb][0], bv2 = B.sb[j][nb][1];
+            sc = __uint_as_float(e ? sv & 0xFFFF0000u : sv << 16);
+            bi = __uint_as_float(e ? bv2 & 0xFFFF0000u : bv2 << 16);
+          } else {
+            sc = __uint_as_float(B.sb[j][nb][e] << 16);
+            bi = __uint_as_float(B.sb[j][nb][e] & 0xFFFF0000u);
+          }
           const float b2 = fmaf(BITS == 8 ? 0.f : -128.f, sc, bi);
 #pragma unroll
           for (int r = 0; r < RPL; ++r)
@@ -544,10 +597,38 @@ hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
   dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
   const uint8_t* t = static_cast<const uint8_t*>(tw);
   if (gs == 32)
-    qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW><<<grid, 64 * WPB, 0, s>>>(x, M, K, t, N, bias, y);
+    qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW, false><<<grid, 64 * WPB, 0, s>>>(
+        x, M, K, t, N, bias, y, nullptr, nullptr, nullptr, 0);
   else
-    qmv_tiled_kernel<BITS, MT, 1, NH, WPB, SPW><<<grid, 64 * WPB, 0, s>>>(x, M, K, t, N, bias, y);
+    qmv_tiled_kernel<BITS, MT, 1, NH, WPB, SPW, false><<<grid, 64 * WPB, 0, s>>>(
+        x, M, K, t, N, bias, y, nullptr, nullptr, nullptr, 0);
   return hipGetLastError();
+}
+
+// The same kernel reading the MLX layout in place (K % 64 == 0).
+template <int BITS, int MT>
+hipError_t run_qmv_mlx(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                       const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                       hipStream_t s) {
+  constexpr int NH = kTiledNH, WPB = kTiledWaves, SPW = kTiledSPW;
+  dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
+  if (gs == 32)
+    qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW, true><<<grid, 64 * WPB, 0, s>>>(
+        x, M, K, nullptr, N, bias, y, wq, sc, bi, 0);
+  else
+    qmv_tiled_kernel<BITS, MT, 1, NH, WPB, SPW, true><<<grid, 64 * WPB, 0, s>>>(
+        x, M, K, nullptr, N, bias, y, wq, sc, bi, gs == 128 ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <int BITS>
+hipError_t pick_mt_mlx(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
+                       const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
+                       hipStream_t s) {
+  if (M <= 1) return run_qmv_mlx<BITS, 1>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (M <= 2) return run_qmv_mlx<BITS, 2>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  if (M <= 4) return run_qmv_mlx<BITS, 4>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
+  return run_qmv_mlx<BITS, 8>(x, M, K, wq, sc, bi, N, gs, bias, y, s);
 }
 
 template <int BITS>
@@ -567,6 +648,19 @@ hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,
                       const uint16_t* scales, const uint16_t* biases, int N, int gs, int bits,
                       const uint16_t* bias, uint16_t* y, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
+  // whole 64-code steps: the step kernel over the MLX layout; otherwise (K an odd
+  // multiple of 32, gs = 32) the lane-per-chunk kernel above
+  if (K % 64 == 0) {
+    switch (bits) {
+      case 2: return pick_mt_mlx<2>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      case 3: return pick_mt_mlx<3>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      case 4: return pick_mt_mlx<4>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      case 5: return pick_mt_mlx<5>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      case 6: return pick_mt_mlx<6>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      case 8: return pick_mt_mlx<8>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (bits) {
     case 2: return pick_mt<2>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
     case 3: return pick_mt<3>(x, M, K, wq, scales, biases, N, gs, bias, y, s);
