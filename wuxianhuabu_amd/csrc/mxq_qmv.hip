@@ -610,7 +610,11 @@ template <int BITS, int MT>
 hipError_t run_qmv_mlx(const uint16_t* x, int M, int K, const uint32_t* wq, const uint16_t* sc,
                        const uint16_t* bi, int N, int gs, const uint16_t* bias, uint16_t* y,
                        hipStream_t s) {
-  constexpr int NH = kTiledNH, WPB = kTiledWaves, SPW = kTiledSPW;
+  // batches of 4 steps: a batch reads 4 x 8 * BITS contiguous bytes of each row (192 B
+  // at 6 bits), so fewer of a row's 128-byte lines are split between batches
+  // (M = 2, N = 24576: 31.4 us against 32.8 us with 2 steps; 8 or 16 steps, two
+  // record halves per workgroup or 2 waves per workgroup were slower)
+  constexpr int NH = 1, WPB = 4, SPW = 4;
   dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
   if (gs == 32)
     qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW, true><<<grid, 64 * WPB, 0, s>>>(
