@@ -6,11 +6,16 @@
 // tied-embedding logits (M = 1, N = 262144,
 // `model/3模块/ltx2.5专属/gemma4文本-(ltx专属).swift:306-312`).
 //
-// HBM-bound: every packed weight byte is read exactly once, with coalesced
-// loads (consecutive lanes read consecutive 16-code chunks of a row). No MFMA.
-// Split-K: the K dimension of each row is spread over the 64 lanes of a wave
-// (and, when N is small, over the 4 waves of a block); partial sums meet in
-// wavefront shuffles and, across waves, in LDS.
+// HBM-bound: every packed weight byte is read once. Two kernels:
+//   * qmv_tiled_kernel (below): one workgroup per 32-row half of a 64-row block,
+//     64-code K steps, the dot products on the matrix cores. It reads the tiled
+//     layout, or (MLX = true) the MLX layout in place when K % 64 == 0;
+//   * qmv_kernel (this section): the MLX layout for any K (K an odd multiple of
+//     32 included), with coalesced loads (consecutive lanes read consecutive
+//     16-code chunks of a row) and no MFMA.
+// qmv_kernel splits K: the K dimension of each row is spread over the 64 lanes
+// of a wave (and, when N is small, over the 4 waves of a block); partial sums
+// meet in wavefront shuffles and, across waves, in LDS.
 //
 // Per 16-code chunk the affine form is factored:
 //   sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k
