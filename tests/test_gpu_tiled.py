@@ -152,6 +152,25 @@ def test_tiled_qmv_parity(dev, O, bits, gs, M):
     assert spec_metric(y, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
+def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
+    """For K % 64 == 0 the MLX-layout GEMV is the tiled GEMV kernel reading the
+    MLX layout in place: same wave split, same per-step arithmetic, so the
+    outputs agree bit for bit (ragged N, every token count)."""
+    N, K = 200, 1024
+    for M in (1, 2, 3, 5, 8):
+        x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 17 + gs + M,
+                                      with_bias=(M % 2 == 1))
+        tw = _tile(dev, wq, s, b, gs, bits)
+        y_t = _tiled_run(dev, x, tw, bias, path="qmv")
+        y_m = mx.quantized_matmul(dev_bf16(x, dev), dev_words(wq, dev), dev_bf16(s, dev),
+                                  dev_bf16(b, dev), group_size=gs, bits=bits,
+                                  bias=None if bias is None else dev_bf16(bias, dev), path="qmv")
+        np.testing.assert_array_equal(host_bf16(y_t), host_bf16(y_m),
+                                      err_msg=f"bits={bits} gs={gs} M={M}")
+
+
 @pytest.mark.parametrize("N,K", [(1, 64), (63, 128), (65, 4096), (24576 // 8, 4096),
                                  (300, 11264)])
 def test_tiled_qmv_shapes(dev, O, N, K):
