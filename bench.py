@@ -542,8 +542,32 @@ def main():
         a = sum(p) / len(p)
         fl = sum(2.0 * M * N * K for _, M, K, N in C4_CHAIN)
         extra["c4 4-bit DiT block chain"] = {"ms": a, "tflops": fl / a / 1e9}
-        res["extra"] = extra
         del chain
+        # Gemma-4 tied-embedding logits (`gemma4文本-(ltx专属).swift:306-312`): M = 1,
+        # K = 3840, N = 262144, 4-bit gs64: 566 MB per token, above the 256 MB Infinity
+        # Cache, so one copy misses it. Both layouts: tiled (QuantizedLinear) and the
+        # MLX layout read in place (quantizedMatmul on the stored triple).
+        lg = dict(M=1, K=3840, N=262144, gs=64, bits=4, seed=60)
+        lx, lwq, ls_, lb = make_inputs(torch, mx, lg, dev)
+        ltw = mx.tile(lwq, ls_, lb, lg["gs"], lg["bits"])
+        ly = torch.empty(1, lg["N"], dtype=torch.bfloat16, device=dev)
+        lbytes = gemv_bytes(lg)
+
+        def logits_tiled(_i):
+            ok(L.mxq_qmv_tiled(P(lx), 1, lg["K"], P(ltw.data), lg["N"], lg["gs"], lg["bits"], None,
+                               P(ly), cur()))
+
+        def logits_mlx(_i):
+            ok(L.mxq_qmv(P(lx), 1, lg["K"], P(lwq), P(ls_), P(lb), lg["N"], lg["gs"], lg["bits"],
+                         None, P(ly), cur()))
+
+        for nm, fn in (("tiled", logits_tiled), ("MLX layout", logits_mlx)):
+            p, t = time_graph(torch, fn, 20, max(5, steps // 3))
+            a = sum(p) / len(p)
+            extra[f"gemma4 logits GEMV 4-bit M=1 K=3840 N=262144, {nm}"] = {
+                "us": a * 1e3, "gbs": lbytes / (a * 1e-3) / 1e9, "bytes": lbytes}
+        del lx, lwq, ls_, lb, ltw, ly
+        res["extra"] = extra
 
     # ---------------- CPU leg (oracle) ----------------
     if not args.no_cpu:
