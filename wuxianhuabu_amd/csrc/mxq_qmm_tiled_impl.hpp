@@ -587,37 +587,51 @@ hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
 // 256 features): the weight loads and unpacking do not shrink with the tile.
 constexpr double kTileCost64 = 0.6, kTileCost128 = 0.75;
 
-// Token tiles of 256 rows (64 or 128 for small M). When M % 256 leaves a
-// remainder of at most 128 rows and the full tiles alone fill whole rounds of
-// the CUs better, the remainder runs as a second launch with smaller tiles
-// instead of as a last round of mostly empty 256-row tiles.
+// Token tiles of 64, 128 or 256 rows, chosen by estimated time: rounds of
+// tiles over the CUs times the relative cost of one tile. Small problems (few
+// 256-row tiles, e.g. M = 256 with N = 2048: 8 tiles for 256 CUs) take the
+// smaller tiles, which spread the same work over more CUs. When M % 256
+// leaves a remainder of at most 128 rows and the full tiles alone fill whole
+// rounds better, the remainder runs as a second launch with smaller tiles
+// instead of as a last round of mostly empty 256-row tiles. Every tile height
+// accumulates each output in the same order, so the choice never changes a
+// result bit.
 template <int BITS, int GP>
 hipError_t pick_rows(const uint16_t* x, int M, int K, const void* tw, int N,
                      const uint16_t* bias, int act, const Lora& lo, uint16_t* y,
                      hipStream_t s) {
   if (M <= 64) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
-  if (M <= 128) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  const int64_t cus = cu_count(), n_tiles = (N + kRows - 1) / kRows;
+  auto rounds = [&](int64_t tiles) { return static_cast<double>((tiles + cus - 1) / cus); };
+  const double t64 = rounds((M + 63) / 64 * n_tiles) * kTileCost64;
+  const double t128 = rounds((M + 127) / 128 * n_tiles) * kTileCost128;
+  if (M <= 128) {
+    if (t64 < t128) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+    return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  }
   const int full = M / 256, rem = M % 256;
+  const int64_t t_full = static_cast<int64_t>(full) * n_tiles;
+  const double one = rounds((M + 255) / 256 * n_tiles);
+  double t256 = one;
+  bool split = false;
   if (rem > 0 && rem <= 128) {
-    const int64_t cus = cu_count(), n_tiles = (N + kRows - 1) / kRows;
-    const int64_t t_full = static_cast<int64_t>(full) * n_tiles;
-    const double one = static_cast<double>((t_full + n_tiles + cus - 1) / cus);
-    const double two = static_cast<double>((t_full + cus - 1) / cus) +
-                       static_cast<double>((n_tiles + cus - 1) / cus) *
-                           (rem <= 64 ? kTileCost64 : kTileCost128);
+    const double two = rounds(t_full) + rounds(n_tiles) * (rem <= 64 ? kTileCost64 : kTileCost128);
     if (two < one) {
-      const hipError_t e =
-          run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, act, lo, y, s);
-      if (e != hipSuccess) return e;
-      const int64_t r0 = static_cast<int64_t>(full) * 256;
-      const int64_t ldy = act == MXQ_ACT_SWIGLU ? N / 2 : N;
-      const Lora rl{lo.xa ? lo.xa + r0 * lo.R : nullptr, lo.bt, lo.R};
-      if (rem <= 64)
-        return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy,
-                                       s);
-      return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy,
-                                      s);
+      t256 = two;
+      split = true;
     }
+  }
+  if (t64 < t256 && t64 <= t128) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  if (t128 < t256) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  if (split) {
+    const hipError_t e = run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, act, lo, y, s);
+    if (e != hipSuccess) return e;
+    const int64_t r0 = static_cast<int64_t>(full) * 256;
+    const int64_t ldy = act == MXQ_ACT_SWIGLU ? N / 2 : N;
+    const Lora rl{lo.xa ? lo.xa + r0 * lo.R : nullptr, lo.bt, lo.R};
+    if (rem <= 64)
+      return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy, s);
+    return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy, s);
   }
   return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, act, lo, y, s);
 }
