@@ -295,6 +295,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t zero_chunk[WPB][SPW * 128];
   __shared__ float xsum_all[WPB][NSUM];
 
+  // Naming an AGPR keeps the MFMA results in AGPRs. A kernel that names none may
+  // be given VGPR-form MFMAs, and with 8-wave workgroups the compiler then wrote
+  // some MFMA results over their own A or B operand registers, which gave
+  // timing-dependent wrong sums.
+  asm volatile("" ::: "a0");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
