@@ -62,6 +62,22 @@ def test_qmv_parity(dev, O, bits, gs, M):
     assert_tight(y, ref, f"qmv bits={bits} gs={gs} M={M}")
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+@pytest.mark.parametrize("N,K", [(96, 96), (40, 544), (17000, 160)])
+def test_qmv_k_odd_multiple_of_32(dev, O, bits, M, N, K):
+    """K an odd multiple of 32 (gs = 32) does not fill whole 64-code steps: the
+    GEMV takes the lane-per-chunk kernel, with the K range split over the 4 waves
+    (small N) or one wave per row set (N = 17000 at M <= 2: 8-row sets, >= 2048 waves)."""
+    gs = 32
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 7 + M + K,
+                                  with_bias=(M % 2 == 0))
+    y = run(dev, x, wq, s, b, bias, gs, bits, path="qmv")
+    ref = O.qmm_f64(x, wq, s, b, gs, bits, bias=bias)
+    assert_tight(y, ref, f"qmv K={K} bits={bits} M={M} N={N}")
+    assert spec_metric(y, ref) <= 2e-2
+
+
 @pytest.mark.parametrize("N", [1, 32, 33, 4000, 6000])
 def test_qmv_row_counts_and_split(dev, O, N):
     """Small N uses the 4-wave K split, large N one wave per row set."""
