@@ -379,6 +379,23 @@ def main():
         res["qmm_mlx_layout"] = {"kernel_avg_ms": mavg,
                                  "tflops": 2.0 * c["M"] * c["N"] * c["K"] / (mavg * 1e-3) / 1e12}
         print(f"[bench] qmm (MLX layout): avg {mavg:.3f} ms", file=sys.stderr, flush=True)
+        # the same MLX-layout call with a workspace: the weight is tiled into it, then the
+        # tiled kernel runs (both launches timed, every call)
+        ws = torch.empty(int(L.mxq_quantized_matmul_workspace_size(c["M"], c["N"], c["K"], c["gs"],
+                                                                   c["bits"])),
+                         dtype=torch.uint8, device=dev)
+
+        def qmm_ws_launch(_i):
+            ok(L.mxq_quantized_matmul_ws(P(x), c["M"], c["K"], P(wq), P(s), P(b), c["N"], 1,
+                                         c["gs"], c["bits"], None, P(y), P(ws), ws.numel(), cur()))
+
+        wper, _ = time_launches(torch, qmm_ws_launch, max(5, steps // 3), 2)
+        wavg = sum(wper) / len(wper)
+        res["qmm_mlx_layout_workspace"] = {
+            "ms": wavg, "tflops": 2.0 * c["M"] * c["N"] * c["K"] / (wavg * 1e-3) / 1e12,
+            "workspace_bytes": ws.numel(), "note": "mxq_quantized_matmul_ws: mxq_tile + tiled qmm"}
+        print(f"[bench] qmm (MLX layout, workspace): avg {wavg:.3f} ms", file=sys.stderr, flush=True)
+        del ws
     per, total = time_launches(torch, qmm_launch, steps, warmup)
     flop = 2.0 * c["M"] * c["N"] * c["K"]
     per_sorted = sorted(per)

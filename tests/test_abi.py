@@ -168,3 +168,18 @@ def test_header_candidates_include_six_bit():
     assert weights.header_candidates(768, 64) == [(3, 128), (6, 64)]
     # the shape relation alone is ambiguous for 4-bit files
     assert weights.header_candidates(512, 64) == [(2, 128), (4, 64), (8, 32)]
+
+
+def test_matmul_workspace_size(mxq_lib):
+    """The workspace is the tiled copy of the weight, only where tiling pays off:
+    M >= 1024 and K % 64 == 0 (every width; the results are bit-identical)."""
+    L = mxq_lib
+    ws = L.mxq_quantized_matmul_workspace_size
+    assert ws(14400, 16384, 4096, 64, 6) == L.mxq_tiled_bytes(16384, 4096, 64, 6) > 0
+    for bits in (2, 3, 4, 5, 8):
+        assert ws(1024, 300, 640, 32, bits) == L.mxq_tiled_bytes(300, 640, 32, bits)
+    assert ws(1023, 16384, 4096, 64, 6) == 0     # too few tokens
+    assert ws(4096, 300, 96, 32, 6) == 0         # K not a multiple of 64
+    assert ws(4096, 0, 640, 64, 4) == 0
+    assert ws(4096, 300, 640, 64, 7) < 0         # unsupported width: an MXQ_ERR_* code
+    assert ws(-1, 300, 640, 64, 4) < 0

@@ -64,7 +64,9 @@ def _check(O, x, wq, s, b, y, rows, gs, bits, what, exact_only=False):
 def _both_layouts(dev, O, M, K, N, bits, seed_x, seed_w, nrows, what, gelu=False):
     x = _acts(dev, M, K, seed_x, gelu)
     wq, s, b = _weights(dev, N, K, seed_w, bits)
-    y_mlx = mx.quantized_matmul(x, wq, s, b, group_size=64, bits=bits)
+    # the MLX-layout kernels themselves (path="auto" tiles the weight first at large M)
+    y_mlx = mx.quantized_matmul(x, wq, s, b, group_size=64, bits=bits,
+                                path="qmv" if M <= 8 else "qmm")
     tw = mx.tile(wq, s, b, 64, bits)
     y_t = mx.tiled_matmul(x, tw)
     rows = _rows(M, nrows, seed_x)
@@ -107,7 +109,7 @@ def test_c4_chain_4bit(dev, O):
         layers.append((name, M, K, N, wq, s, b, mx.tile(wq, s, b, 64, 4)))
     for i, (name, M, K, N, wq, s, b, tw) in enumerate(layers):
         x = _acts(dev, M, K, 1004 + 100 * i, gelu=(name == "down"))
-        y_mlx = mx.quantized_matmul(x, wq, s, b, group_size=64, bits=4)
+        y_mlx = mx.quantized_matmul(x, wq, s, b, group_size=64, bits=4, path="qmm")
         y_t = mx.tiled_matmul(x, tw)
         assert torch.equal(y_mlx, y_t), f"c4 {name}: layouts differ"
         _check(O, x, wq, s, b, y_t, _rows(M, 16, 1004 + i), 64, 4, f"c4 {name}")

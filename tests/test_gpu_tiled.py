@@ -154,6 +154,38 @@ def test_tiled_qmv_parity(dev, O, bits, gs, M):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("gs", GS)
+def test_workspace_matmul_bit_identical(dev, O, bits, gs):
+    """quantized_matmul(path="auto") at M >= 1024 tiles the MLX-layout weight into a
+    workspace and runs the tiled kernel: the same bits as the MLX-layout MFMA kernel.
+    A workspace one byte short, or none, takes mxq_quantized_matmul itself."""
+    import ctypes
+    M, N, K = 1100, 300, 640
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 13 + gs, with_bias=True)
+    xd, wd, sd, bd, biasd = (dev_bf16(x, dev), dev_words(wq, dev), dev_bf16(s, dev),
+                             dev_bf16(b, dev), dev_bf16(bias, dev))
+    y_auto = mx.quantized_matmul(xd, wd, sd, bd, group_size=gs, bits=bits, bias=biasd)
+    y_qmm = mx.quantized_matmul(xd, wd, sd, bd, group_size=gs, bits=bits, bias=biasd, path="qmm")
+    np.testing.assert_array_equal(host_bf16(y_auto), host_bf16(y_qmm))
+    L = mx.lib()
+    need = L.mxq_quantized_matmul_workspace_size(M, N, K, gs, bits)
+    assert need == L.mxq_tiled_bytes(N, K, gs, bits) > 0
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    for nbytes in (need, need - 1, 0):
+        y = torch.empty_like(y_qmm)
+        assert L.mxq_quantized_matmul_ws(P(xd), M, K, P(wd), P(sd), P(bd), N, 1, gs, bits,
+                                         P(biasd), P(y), P(ws), nbytes, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_qmm), f"workspace {nbytes} of {need} bytes"
+    rows = np.arange(0, M, 37)
+    assert_tight(host_f32_of_bf16(y_auto)[rows],
+                 O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows),
+                 f"workspace matmul bits={bits} gs={gs}")
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
 def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
     """For K % 64 == 0 the MLX-layout GEMV is the tiled GEMV kernel reading the
     MLX layout in place: same wave split, same per-step arithmetic, so the

@@ -35,6 +35,9 @@ SIGNATURES = {
     "mxq_unpack": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "mxq_quantized_matmul": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _int,
                                     _vp, _vp, _vp]),
+    "mxq_quantized_matmul_workspace_size": (_i64, [_i64, _i64, _i64, _int, _int]),
+    "mxq_quantized_matmul_ws": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _int,
+                                       _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "mxq_qmm": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_qmv": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),

@@ -411,6 +411,39 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
   return mxq_qmm(x, M, K, wq, scales, biases, N, group_size, bits, bias, y, stream);
 }
 
+int64_t mxq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size,
+                                            int bits) {
+  int rc = check_bits_gs("quantized_matmul", bits, group_size, K);
+  if (rc) return rc;
+  if (M < 0 || N < 0 || K < 0) return fail(MXQ_ERR_INVALID, "[quantized_matmul] Negative dimension.");
+  ok();
+  // Tiling reads and writes the weight once; from about this many tokens the tiled MFMA
+  // kernel saves more than that (the MLX-layout kernel takes about 1.7x its time). Both
+  // MFMA kernels accumulate each output in the same order: the result bits are the same.
+  constexpr int64_t kTileMinM = 1024;
+  if (M < kTileMinM || M > INT32_MAX || N == 0 || N > INT32_MAX || K == 0 || K % 64 != 0 ||
+      K > INT32_MAX || !mxq::detail::qmm_supports_bits(bits))
+    return 0;
+  return mxq::tiled::total_bytes(N, K, group_size, bits);
+}
+
+int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                            const void* scales, const void* biases, int64_t N, int transpose,
+                            int group_size, int bits, const void* bias, void* y, void* workspace,
+                            size_t ws_bytes, mxq_stream stream) {
+  const int64_t need = mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits);
+  if (transpose != 1 || need <= 0 || !workspace || ws_bytes < static_cast<size_t>(need) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+    return mxq_quantized_matmul(x, M, K, wq, scales, biases, N, transpose, group_size, bits, bias,
+                                y, stream);
+  int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
+                        bias, y);
+  if (rc) return rc;
+  rc = mxq_tile(wq, scales, biases, N, K, group_size, bits, workspace, stream);
+  if (rc) return rc;
+  return mxq_qmm_tiled(x, M, K, workspace, N, group_size, bits, bias, y, stream);
+}
+
 }  // extern "C"
 
 // ---- row-wise ops of the DiT block (mxq_blockops.hip)

@@ -170,6 +170,9 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
     """y [..., N] = x [..., K] @ dequantized(w)^T (+ bias), bf16 in/out, fp32 accumulate.
 
     path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv" to force a kernel.
+    With "auto" and many tokens (mxq_quantized_matmul_workspace_size > 0) the weight is
+    tiled into a temporary buffer first and the tiled MFMA kernel runs: the same
+    result bits, in less time.
     """
     op = "quantized_matmul"
     x, w, scales, biases, bias, N, K = _matmul_shapes(op, x, w, scales, biases, group_size,
@@ -180,8 +183,13 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
     L = _lib.lib()
     args = (_ptr(x), M, K, _ptr(w), _ptr(scales), _ptr(biases), N)
     if path == "auto":
-        rc = L.mxq_quantized_matmul(*args, 1 if transpose else 0, group_size, bits, _ptr(bias),
-                                    _ptr(y), _stream(x))
+        ws_bytes = L.mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits) \
+            if transpose else 0
+        ws = torch.empty(max(int(ws_bytes), 0), dtype=torch.uint8, device=x.device) \
+            if ws_bytes > 0 else None
+        rc = L.mxq_quantized_matmul_ws(*args, 1 if transpose else 0, group_size, bits,
+                                       _ptr(bias), _ptr(y), _ptr(ws),
+                                       0 if ws is None else ws.numel(), _stream(x))
     elif not transpose:
         raise NotImplementedError("[quantized_matmul] transpose=False is not implemented.")
     elif path == "qmm":
