@@ -183,20 +183,35 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
   const int64_t row = pairs ? h * (N / 2) + rb * 32 + r : rb * 64 + h * 32 + r;
   const bool valid = pairs ? rb * 32 + r < N / 2 : row < N;
   const int64_t W = K / 32 * BITS;
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  // the run's BITS words (dword-aligned in the MLX row): 16-byte loads, then the
+  // remainder as one 8-byte, 4-byte or three 4-byte loads
   uint32_t words[BITS];
   const uint32_t* src = wq + (valid ? row : 0) * W + (kk * 64 + 32 * g) / 32 * BITS;
 #pragma unroll
-  for (int i = 0; i < BITS; ++i) words[i] = valid ? src[i] : 0u;
+  for (int p = 0; p < FP; ++p) {
+    const u32x4 v = valid ? *reinterpret_cast<const u32x4*>(src + 4 * p) : u32x4{0u, 0u, 0u, 0u};
+    words[4 * p] = v.x; words[4 * p + 1] = v.y; words[4 * p + 2] = v.z; words[4 * p + 3] = v.w;
+  }
+  if constexpr (RW == 2) {
+    const u32x2 v = valid ? *reinterpret_cast<const u32x2*>(src + 4 * FP) : u32x2{0u, 0u};
+    words[4 * FP] = v.x; words[4 * FP + 1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < RW; ++i) words[4 * FP + i] = valid ? src[4 * FP + i] : 0u;
+  }
   uint8_t* rec = out + rk * tiled::record_bytes(BITS, gs);
   uint8_t* half = rec + h * tiled::half_bytes(BITS);
-  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  // one 16-byte store per plane (a wave writes 1 KiB of a plane contiguously); the
+  // remainder plane holds RW words per unit
 #pragma unroll
-  for (int p = 0; p < FP; ++p) {
-    uint32_t* d = reinterpret_cast<uint32_t*>(half + p * 1024 + u * 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = words[4 * p + i];
-  }
-  if constexpr (RW > 0) {
+  for (int p = 0; p < FP; ++p)
+    *reinterpret_cast<u32x4a*>(half + p * 1024 + u * 16) =
+        u32x4a{words[4 * p], words[4 * p + 1], words[4 * p + 2], words[4 * p + 3]};
+  if constexpr (RW == 2) {
+    typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u32x2a*>(half + FP * 1024 + u * 8) = u32x2a{words[4 * FP], words[4 * FP + 1]};
+  } else if constexpr (RW > 0) {
     uint32_t* d = reinterpret_cast<uint32_t*>(half + FP * 1024 + u * 4 * RW);
 #pragma unroll
     for (int i = 0; i < RW; ++i) d[i] = words[4 * FP + i];
