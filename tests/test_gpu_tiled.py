@@ -189,9 +189,13 @@ def test_workspace_matmul_bit_identical(dev, O, bits, gs):
 def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
     """For K % 64 == 0 the MLX-layout GEMV is the tiled GEMV kernel reading the
     MLX layout in place: same wave split, same per-step arithmetic, so the
-    outputs agree bit for bit (ragged N, every token count)."""
-    N, K = 200, 1024
-    for M in (1, 2, 3, 5, 8):
+    outputs agree bit for bit (ragged N, every token count). K = 192 gives rows
+    of 24 * bits bytes, not whole 16-byte chunks for odd widths: the batch's
+    coalesced loads then straddle row ends."""
+    for (M, N, K) in [(1, 200, 1024), (2, 200, 1024), (3, 200, 1024), (5, 200, 1024),
+                      (8, 200, 1024), (2, 130, 192), (7, 130, 192)]:
+        if K % gs:
+            continue
         x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 17 + gs + M,
                                       with_bias=(M % 2 == 1))
         tw = _tile(dev, wq, s, b, gs, bits)
@@ -200,7 +204,7 @@ def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
                                   dev_bf16(b, dev), group_size=gs, bits=bits,
                                   bias=None if bias is None else dev_bf16(bias, dev), path="qmv")
         np.testing.assert_array_equal(host_bf16(y_t), host_bf16(y_m),
-                                      err_msg=f"bits={bits} gs={gs} M={M}")
+                                      err_msg=f"bits={bits} gs={gs} M={M} K={K}")
 
 
 @pytest.mark.parametrize("N,K", [(1, 64), (63, 128), (65, 4096), (24576 // 8, 4096),

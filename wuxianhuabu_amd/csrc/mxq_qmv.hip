@@ -270,10 +270,12 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // steps per wave; MT <= 8 tokens.
 //
 // MLX: the same kernel over the MLX layout itself (wq [N, K*BITS/32], scales and
-// biases [N, K/gs], K % 64 == 0), for callers that keep no tiled copy. Lane
-// (l32, g2) of row block rb, half h, reads the BITS words of codes
-// [64k + 32 g2, +32) of row 64 rb + 32 h + l32 (a run of 32 codes is BITS whole
-// words) and that row's scale and bias of step k's group(s), then everything
+// biases [N, K/gs], K % 64 == 0), for callers that keep no tiled copy. A wave
+// loads a batch's bytes of its 32 rows (SPW * 8 * BITS contiguous bytes per row)
+// with consecutive lanes on consecutive 16-byte chunks, stages them in its own
+// LDS region, and lane (l32, g2) reads back the BITS words of codes
+// [64k + 32 g2, +32) of its row l32 (a run of 32 codes is BITS whole words);
+// it loads that row's scale and bias of step k's group(s) itself. Everything
 // else is shared. gshift = log2(gs / 64) for gs >= 64.
 template <int BITS, int MT, int GP, int NH, int WPB, int SPW, bool MLX>
 __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
@@ -294,6 +296,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t lds[WPB * XW];
   __shared__ __attribute__((aligned(16))) uint8_t zero_chunk[WPB][SPW * 128];
   __shared__ float xsum_all[WPB][NSUM];
+  // MLX layout: a batch's weight bytes of the wave's rows (CPR 16-byte chunks of each
+  // row, loaded with consecutive lanes on consecutive chunks), staged row by row at a
+  // padded stride and read back as each lane's runs
+  constexpr int CPR = SPW * BITS / 2;          // 16-byte chunks of a row per batch
+  constexpr int NCL = 32 * CPR / 64;           // coalesced 16-byte loads per lane per half
+  constexpr int RSTR = CPR * 16 + 16;          // staged row stride
+  static_assert(!MLX || (SPW * BITS) % 4 == 0, "whole loads of 64 lanes per batch");
+  __shared__ __attribute__((aligned(16))) uint8_t wl_all[WPB][MLX ? NH * 32 * RSTR : 16];
 
   // Naming an AGPR keeps the MFMA results in AGPRs. A kernel that names none may
   // be given VGPR-form MFMAs, and with 8-wave workgroups the compiler then wrote
@@ -318,6 +328,9 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // range check covers
   __amdgpu_buffer_rsrc_t wrs, srs, brs;
   int wvo[NH], rvo[NH], svo[NH];
+  // MLX: piece i of half nb; lane l loads chunk q % CPR of row q / CPR (q = 64 i + l)
+  // of the batch: cro = its row's offset, cco = the chunk's, clo = where it is staged
+  int cro[MLX ? NH : 1][MLX ? NCL : 1], cco[MLX ? NCL : 1], clo[MLX ? NCL : 1];
   if constexpr (MLX) {
     const int rowb = K / 8 * BITS;                      // bytes per weight row
     const int G = GP == 2 ? K >> 5 : K >> (6 + gshift);  // groups per row
@@ -332,6 +345,17 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
       wvo[nb] = r * rowb + g2 * BITS * 4;
       rvo[nb] = wvo[nb] + FP * 16;
       svo[nb] = r * G * 2;
+#pragma unroll
+      for (int i = 0; i < NCL; ++i) {
+        const int q = 64 * i + lane;
+        cro[nb][i] = min((h0 + nb) * 32 + q / CPR, rows - 1) * rowb;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NCL; ++i) {
+      const int q = 64 * i + lane;
+      cco[i] = (q % CPR) * 16;
+      clo[i] = (q / CPR) * RSTR + (q % CPR) * 16;
     }
   } else {
     wrs = ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
@@ -390,7 +414,8 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // are split where used, so the loads stay in flight until then.
   struct Batch {
     v4u_t x[XLOADS];
-    uint32_t w[SPW][NH][BITS];
+    uint32_t w[MLX ? 1 : SPW][NH][BITS];     // tiled: each step's unit words
+    v4u_t wc[MLX ? NH : 1][MLX ? NCL : 1];   // MLX: the batch's row chunks
     uint32_t sb[SPW][NH][MLX ? 2 : GP];
   };
   auto load = [&](Batch& B, int b0) __attribute__((always_inline)) {
@@ -409,6 +434,18 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
             xrs, (m * K + st * 64) * 2 + ((o / 16) % 8) * 16, 0, 0);
       }
     }
+    if constexpr (MLX) {
+      // the batch's bytes of each row. Chunks past a row's end hold the next row's
+      // bytes or, past the last row, zeros (the whole offset is in the vector offset,
+      // which the buffer range check covers); they are staged where steps past K
+      // would be, and never used.
+      const int sb0 = __builtin_amdgcn_readfirstlane(b0 * 8 * BITS);
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb)
+#pragma unroll
+        for (int i = 0; i < NCL; ++i)
+          B.wc[nb][i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, cro[nb][i] + sb0 + cco[i], 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       // uniform, kept in an SGPR (a VGPR soffset would become a readfirstlane loop)
@@ -416,22 +453,23 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
       const int so = __builtin_amdgcn_readfirstlane(MLX ? kj * 8 * BITS : kj * RB);
 #pragma unroll
       for (int nb = 0; nb < NH; ++nb) {
+        if constexpr (!MLX) {
 #pragma unroll
-        for (int p = 0; p < FP; ++p) {
-          const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * (MLX ? 16 : 1024),
-                                                                so, 0);
-          B.w[j][nb][4 * p] = v.x; B.w[j][nb][4 * p + 1] = v.y;
-          B.w[j][nb][4 * p + 2] = v.z; B.w[j][nb][4 * p + 3] = v.w;
-        }
-        if constexpr (RW == 1) {
-          B.w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
-        } else if constexpr (RW == 2) {
-          const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
-          B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
-        } else if constexpr (RW == 3) {
-          const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
-          B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
-          B.w[j][nb][4 * FP + 2] = v.z;
+          for (int p = 0; p < FP; ++p) {
+            const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+            B.w[j][nb][4 * p] = v.x; B.w[j][nb][4 * p + 1] = v.y;
+            B.w[j][nb][4 * p + 2] = v.z; B.w[j][nb][4 * p + 3] = v.w;
+          }
+          if constexpr (RW == 1) {
+            B.w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+          } else if constexpr (RW == 2) {
+            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
+            B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
+          } else if constexpr (RW == 3) {
+            const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
+            B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
+            B.w[j][nb][4 * FP + 2] = v.z;
+          }
         }
         if constexpr (MLX) {
           if constexpr (GP == 2) {  // groups 2k and 2k + 1
@@ -460,6 +498,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // FULLB: all SPW steps lie before k_end (true of every batch but a wave's last)
   auto consume = [&](auto fullc, const Batch& B, int b0) __attribute__((always_inline)) {
     constexpr bool FULLB = decltype(fullc)::value;
+    uint8_t* const wl = wl_all[wave];
+    if constexpr (MLX) {  // this wave's own region: its earlier reads of it come first
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb)
+#pragma unroll
+        for (int i = 0; i < NCL; ++i)
+          *reinterpret_cast<v4u_t*>(wl + nb * 32 * RSTR + clo[i]) = B.wc[nb][i];
+    }
 #pragma unroll
     for (int i = 0; i < XLOADS; ++i)
       *reinterpret_cast<v4u_t*>(xw + i * 1024 + lane * 16) = B.x[i];
@@ -499,6 +545,16 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           av[e][c] = *reinterpret_cast<const bf16x8*>(xa[e] + j * 128 + c * 16);
+      // this step's BITS words of the lane's run: tiled, as loaded; MLX, from the
+      // staged rows (row l32, run 2j + g2 of the batch)
+      uint32_t wv[NH][BITS];
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb)
+#pragma unroll
+        for (int i = 0; i < BITS; ++i)
+          wv[nb][i] = MLX ? reinterpret_cast<const uint32_t*>(
+                                wl + nb * 32 * RSTR + l32 * RSTR + (2 * j + g2) * BITS * 4)[i]
+                          : B.w[MLX ? 0 : j][nb][i];
 #pragma unroll
       for (int nb = 0; nb < NH; ++nb) {
         bf16x8 bv[4];
@@ -509,10 +565,10 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           for (int i = 0; i < 4; ++i) {
             const int q = 8 * c + 2 * i;
             if constexpr (BITS == 8)  // codes up to 255: exact bf16 integers, offset 0
-              pr[i] = pack_bf16x2(static_cast<float>(code_at<BITS>(B.w[j][nb], q)),
-                                  static_cast<float>(code_at<BITS>(B.w[j][nb], q + 1)));
+              pr[i] = pack_bf16x2(static_cast<float>(code_at<BITS>(wv[nb], q)),
+                                  static_cast<float>(code_at<BITS>(wv[nb], q + 1)));
             else
-              pr[i] = pair_at<BITS>(B.w[j][nb], q, kPairMask, kMagic);
+              pr[i] = pair_at<BITS>(wv[nb], q, kPairMask, kMagic);
           }
           bv[c] = __builtin_bit_cast(bf16x8, v4u_t{pr[0], pr[1], pr[2], pr[3]});
         }
