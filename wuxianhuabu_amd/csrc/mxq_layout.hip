@@ -228,14 +228,109 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
   }
 }
 
+// The same layout, one workgroup per (row block, group of kTileSteps K steps): the
+// group's bytes of the block's 64 rows are read with consecutive lanes on consecutive
+// 16-byte chunks of a row (rows are contiguous in the MLX layout; tile_kernel's one
+// thread per unit reads 32 rows per load instruction), staged in LDS, then written
+// unit by unit exactly as tile_kernel writes them.
+constexpr int kTileSteps = 4;
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void tile_rows_kernel(const uint32_t* __restrict__ wq,
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint16_t* __restrict__ biases,
+                                                             int64_t N, int64_t K, int gs,
+                                                             bool pairs,
+                                                             uint8_t* __restrict__ out) {
+  constexpr int CPR = kTileSteps * BITS / 2;  // 16-byte chunks of a row per group
+  constexpr int RSTR = CPR * 16 + 16;         // staged row stride
+  __shared__ __attribute__((aligned(16))) uint8_t st[64 * RSTR];
+  const int64_t nk = K / 64;
+  const int64_t ngrp = (nk + kTileSteps - 1) / kTileSteps;
+  const int64_t rb = blockIdx.x / ngrp;
+  const int64_t k0 = (blockIdx.x - rb * ngrp) * kTileSteps;
+  const int64_t rowb = K / 8 * BITS;          // bytes per MLX row
+  const int64_t W = K / 32 * BITS;            // words per MLX row
+  // source row of block row t = 32 h + r; with `pairs`, the halves of row block rb
+  // are rows 32rb + r and N/2 + 32rb + r (gate and up of one output)
+  auto src_row = [&](int t, bool& valid) {
+    const int h = t >> 5, r = t & 31;
+    const int64_t row = pairs ? h * (N / 2) + rb * 32 + r : rb * 64 + t;
+    valid = pairs ? rb * 32 + r < N / 2 : row < N;
+    return row;
+  };
+  for (int c = threadIdx.x; c < 64 * CPR; c += kThreads) {
+    const int t = c / CPR, j = c % CPR;
+    bool valid;
+    const int64_t row = src_row(t, valid);
+    const int64_t off = k0 * 8 * BITS + j * 16;  // byte offset in the row
+    u32x4a v = {0u, 0u, 0u, 0u};
+    if (valid && off < rowb) {  // chunks past the row end belong to steps past K
+      const uint32_t* p = wq + row * W + off / 4;
+      if (off + 16 <= rowb) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+        v = u32x4a{a.x, a.y, a.z, a.w};
+      } else {  // the row ends 8 bytes into this chunk (rowb is a multiple of 8)
+        const u32x2 a = *reinterpret_cast<const u32x2*>(p);
+        v = u32x4a{a.x, a.y, 0u, 0u};
+      }
+    }
+    *reinterpret_cast<u32x4a*>(st + t * RSTR + j * 16) = v;
+  }
+  __syncthreads();
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  for (int e = threadIdx.x; e < 128 * kTileSteps; e += kThreads) {
+    const int u = e & 63, h = (e >> 6) & 1, ks = e >> 7;
+    const int64_t kk = k0 + ks;
+    if (kk >= nk) continue;
+    const int r = u & 31, g = u >> 5, t = h * 32 + r;
+    bool valid;
+    const int64_t row = src_row(t, valid);
+    uint32_t words[BITS];
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + t * RSTR + (2 * ks + g) * BITS * 4);
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) words[i] = sw[i];
+    const int64_t rk = rb * nk + kk;
+    uint8_t* rec = out + rk * tiled::record_bytes(BITS, gs);
+    uint8_t* half = rec + h * tiled::half_bytes(BITS);
+#pragma unroll
+    for (int p = 0; p < FP; ++p)
+      *reinterpret_cast<u32x4a*>(half + p * 1024 + u * 16) =
+          u32x4a{words[4 * p], words[4 * p + 1], words[4 * p + 2], words[4 * p + 3]};
+    if constexpr (RW == 2) {
+      typedef uint32_t u32x2a __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2a*>(half + FP * 1024 + u * 8) = u32x2a{words[4 * FP], words[4 * FP + 1]};
+    } else if constexpr (RW > 0) {
+      uint32_t* d = reinterpret_cast<uint32_t*>(half + FP * 1024 + u * 4 * RW);
+#pragma unroll
+      for (int i = 0; i < RW; ++i) d[i] = words[4 * FP + i];
+    }
+    const int G = tiled::gps(gs);
+    if (G == 2 || g == 0) {
+      const int64_t grp = (kk * 64 + 32 * g) / gs;
+      const int64_t si = (valid ? row : 0) * (K / gs) + grp;
+      const uint32_t sv = valid ? scales[si] : 0u;
+      const uint32_t bv = valid ? biases[si] : 0u;
+      uint32_t* ep = reinterpret_cast<uint32_t*>(rec + tiled::code_bytes(BITS)) +
+                     ((h * 32 + r) * G + (G == 2 ? g : 0));
+      *ep = sv | (bv << 16);
+    }
+  }
+}
+
 template <int BITS>
 struct TileRun {
   static hipError_t run(const uint32_t* wq, const uint16_t* sc, const uint16_t* bi, int64_t N,
                         int64_t K, int gs, bool pairs, void* out, hipStream_t s) {
-    const int64_t items = tiled::row_blocks(N) * (K / 64) * 128;
-    if (items == 0) return hipSuccess;
-    tile_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, sc, bi, N, K, gs, pairs,
-                                                           static_cast<uint8_t*>(out));
+    const int64_t blocks = tiled::row_blocks(N) * ((K / 64 + kTileSteps - 1) / kTileSteps);
+    if (blocks == 0) return hipSuccess;
+    if (blocks > 0x7FFFFFFF) {  // one thread per unit then
+      const int64_t items = tiled::row_blocks(N) * (K / 64) * 128;
+      tile_kernel<BITS><<<grid_for(items), kThreads, 0, s>>>(wq, sc, bi, N, K, gs, pairs,
+                                                             static_cast<uint8_t*>(out));
+    } else {
+      tile_rows_kernel<BITS><<<static_cast<unsigned>(blocks), kThreads, 0, s>>>(
+          wq, sc, bi, N, K, gs, pairs, static_cast<uint8_t*>(out));
+    }
     return hipGetLastError();
   }
 };
