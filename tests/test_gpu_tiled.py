@@ -171,13 +171,15 @@ def test_workspace_matmul_bit_identical(dev, O, bits, gs):
     assert need == L.mxq_tiled_bytes(N, K, gs, bits) > 0
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    ws = torch.empty(need, dtype=torch.uint8, device=dev)
-    for nbytes in (need, need - 1, 0):
+    ws = torch.empty(need + 16, dtype=torch.uint8, device=dev)
+    # full size, one byte short, none, and a workspace that is not 16-byte aligned
+    for nbytes, shift in ((need, 0), (need - 1, 0), (0, 0), (need, 4)):
         y = torch.empty_like(y_qmm)
+        wptr = ctypes.c_void_p(ws.data_ptr() + shift)
         assert L.mxq_quantized_matmul_ws(P(xd), M, K, P(wd), P(sd), P(bd), N, 1, gs, bits,
-                                         P(biasd), P(y), P(ws), nbytes, stream) == 0
+                                         P(biasd), P(y), wptr, nbytes, stream) == 0
         torch.cuda.synchronize()
-        assert torch.equal(y, y_qmm), f"workspace {nbytes} of {need} bytes"
+        assert torch.equal(y, y_qmm), f"workspace {nbytes} of {need} bytes, offset {shift}"
     rows = np.arange(0, M, 37)
     assert_tight(host_f32_of_bf16(y_auto)[rows],
                  O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows),
