@@ -330,11 +330,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   int wvo[NH], rvo[NH], svo[NH];
   // MLX: piece i of half nb; lane l loads chunk q % CPR of row q / CPR (q = 64 i + l)
   // of the batch: cro = its row's offset, cco = the chunk's, clo = where it is staged
-  int cro[MLX ? NH : 1][MLX ? NCL : 1], cco[MLX ? NCL : 1], clo[MLX ? NCL : 1];
+  // packed as (row within the half) | (chunk << 8), unpacked where used
+  int tcq[MLX ? NCL : 1];
+  int rows = 0, rowb = 0;
   if constexpr (MLX) {
-    const int rowb = K / 8 * BITS;                      // bytes per weight row
+    rowb = K / 8 * BITS;                                // bytes per weight row
     const int G = GP == 2 ? K >> 5 : K >> (6 + gshift);  // groups per row
-    const int r0 = rb * 64, rows = min(64, N - r0);
+    const int r0 = rb * 64;
+    rows = min(64, N - r0);
     wrs = ring::make_rsrc(wq + static_cast<int64_t>(r0) * (rowb / 4),
                           static_cast<uint32_t>(rows) * rowb);
     srs = ring::make_rsrc(scs + static_cast<int64_t>(r0) * G, static_cast<uint32_t>(rows) * G * 2);
@@ -345,17 +348,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
       wvo[nb] = r * rowb + g2 * BITS * 4;
       rvo[nb] = wvo[nb] + FP * 16;
       svo[nb] = r * G * 2;
-#pragma unroll
-      for (int i = 0; i < NCL; ++i) {
-        const int q = 64 * i + lane;
-        cro[nb][i] = min((h0 + nb) * 32 + q / CPR, rows - 1) * rowb;
-      }
     }
 #pragma unroll
     for (int i = 0; i < NCL; ++i) {
       const int q = 64 * i + lane;
-      cco[i] = (q % CPR) * 16;
-      clo[i] = (q / CPR) * RSTR + (q % CPR) * 16;
+      tcq[i] = (q / CPR) | ((q % CPR) << 8);
     }
   } else {
     wrs = ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
@@ -441,10 +438,15 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
       // would be, and never used.
       const int sb0 = __builtin_amdgcn_readfirstlane(b0 * 8 * BITS);
 #pragma unroll
-      for (int nb = 0; nb < NH; ++nb)
+      for (int i = 0; i < NCL; ++i) {
+        int tc = tcq[i];
+        asm volatile("" : "+v"(tc));  // unpacked here, not held across the loop
 #pragma unroll
-        for (int i = 0; i < NCL; ++i)
-          B.wc[nb][i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, cro[nb][i] + sb0 + cco[i], 0, 0);
+        for (int nb = 0; nb < NH; ++nb)
+          B.wc[nb][i] = __builtin_amdgcn_raw_buffer_load_b128(
+              wrs, min((h0 + nb) * 32 + (tc & 0xFF), rows - 1) * rowb + sb0 + (tc >> 8) * 16, 0,
+              0);
+      }
     }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -501,10 +503,14 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     uint8_t* const wl = wl_all[wave];
     if constexpr (MLX) {  // this wave's own region: its earlier reads of it come first
 #pragma unroll
-      for (int nb = 0; nb < NH; ++nb)
+      for (int i = 0; i < NCL; ++i) {
+        int tc = tcq[i];
+        asm volatile("" : "+v"(tc));
 #pragma unroll
-        for (int i = 0; i < NCL; ++i)
-          *reinterpret_cast<v4u_t*>(wl + nb * 32 * RSTR + clo[i]) = B.wc[nb][i];
+        for (int nb = 0; nb < NH; ++nb)
+          *reinterpret_cast<v4u_t*>(wl + nb * 32 * RSTR + (tc & 0xFF) * RSTR + (tc >> 8) * 16) =
+              B.wc[nb][i];
+      }
     }
 #pragma unroll
     for (int i = 0; i < XLOADS; ++i)
