@@ -15,6 +15,8 @@
  *                            optional "+ bias" of QuantizedLinear / MfLinear
  *                            `model/minimax h3/H3Common.swift:358-368`,
  *                            `model/3模块/ltx2.5专属/gemma4文本-(ltx专属).swift:306-312`
+ *   mxq_quantized_matmul_ws <- the same call with a caller workspace, into which a
+ *                            large-M call tiles the weight first (same result bits)
  *   mxq_qmm, mxq_qmv      <- the two halves of that op (large-M MFMA kernel,
  *                            small-M GEMV kernel), callable directly
  *   mxq_pack, mxq_unpack  <- the packed-code layout itself (no MLX-Swift
