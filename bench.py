@@ -13,7 +13,9 @@ timing starts. The weights are resident the way QuantizedLinear keeps them: the 
 triple is reordered once, at load time, into the tiled layout (mxq_tile; its one-off
 cost is reported as tile_ms and is not part of a step), and each step runs the tiled
 kernel. The same workloads on the MLX-layout kernels (mxq_qmm / mxq_qmv, no tiling)
-are reported beside them as qmm_mlx_layout / gemv_mlx_layout. The CPU baseline (the oracle's restatement of mlx's CPU quantized
+are reported beside them as qmm_mlx_layout / gemv_mlx_layout, and a dense bf16 library
+GEMM of the headline shape (torch.mm on the dequantized weight) as dense_bf16_library,
+the MFMA rate this board sustains without any unpacking. The CPU baseline (the oracle's restatement of mlx's CPU quantized
 matmul loop, timed on this host) and a sampled-row correctness check run after the
 GPU timing; they are the only part of this file that touches the oracle.
 
@@ -407,6 +409,28 @@ def main():
           f"{achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
     if not args.headline_only:
+        # ---------------- dense bf16 library GEMM, same shape ----------------
+        # A reference point for the MFMA roofline on this board: torch.mm (hipBLASLt) of
+        # the same x with the dequantized weight in bf16 (no unpacking, 2.7x the weight
+        # bytes). Not this library's path.
+        wd = mx.dequantized(wq, s, b, c["gs"], c["bits"], dtype=torch.bfloat16)
+        y_dense = torch.empty_like(y)
+
+        def dense_launch(_i):
+            torch.mm(x, wd.t(), out=y_dense)
+
+        dper, _ = time_launches(torch, dense_launch, max(10, steps // 2), 5)
+        dmed = sorted(dper)[len(dper) // 2]
+        res["dense_bf16_library"] = {
+            "median_ms": dmed, "tflops": flop / (dmed * 1e-3) / 1e12,
+            "frac": flop / (dmed * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "qmm_vs_dense": dmed / med_ms,
+            "note": "torch.mm (hipBLASLt) bf16, x @ dequantized(W)^T, same M, K, N; "
+                    "qmm_vs_dense = dense median / qmm median"}
+        print(f"[bench] dense bf16 library GEMM: median {dmed:.3f} ms (qmm {med_ms:.3f} ms)",
+              file=sys.stderr, flush=True)
+        del wd, y_dense
+
         # ---------------- fused epilogues on the same workload ----------------
         # GELU-tanh (LTX feed-forward) and silu(gate) * up (H3 MLP, the weight's rows read as
         # [gate; up] and tiled in pairs) in the qmm's epilogue, against the unfused chain:
