@@ -122,7 +122,8 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
  * (mxq_tile) and the tiled MFMA kernel runs: bit-identical results, about 1.6x faster
  * at M = 14400, K = 4096, N = 16384. Otherwise, including a NULL or too small
  * workspace, this is mxq_quantized_matmul. Allocates nothing; the workspace is
- * overwritten, and calls sharing one workspace must be ordered on one stream.
+ * overwritten, and calls sharing one workspace must be ordered on one stream. A
+ * workspace that overlaps x, the weight triple, bias or y is MXQ_ERR_INVALID.
  * The size is positive only for M >= 1024 and K % 64 == 0; a negative return is an
  * MXQ_ERR_* code for invalid bits / group_size / K / M. */
 int64_t mxq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size,

@@ -183,3 +183,25 @@ def test_matmul_workspace_size(mxq_lib):
     assert ws(4096, 0, 640, 64, 4) == 0
     assert ws(4096, 300, 640, 64, 7) < 0         # unsupported width: an MXQ_ERR_* code
     assert ws(-1, 300, 640, 64, 4) < 0
+
+
+def test_matmul_workspace_overlap_is_rejected(mxq_lib):
+    """A workspace sharing bytes with an operand is refused before anything is
+    launched (the pointers below are never dereferenced)."""
+    L = mxq_lib
+    M, N, K, gs, bits = 1024, 64, 128, 64, 4
+    need = L.mxq_quantized_matmul_workspace_size(M, N, K, gs, bits)
+    assert need > 0
+    base = 1 << 40
+    x, wq, sc, bi, bias, y = (base + i * (1 << 30) for i in range(6))
+    cases = {
+        "x": x + 64,                                # starts inside x
+        "wq": wq - need + 4 * 16,                   # ends inside the codes
+        "scales": sc, "biases": bi, "bias": bias,
+        "y": y + M * N * 2 - 16,                    # starts in y's last 16 bytes
+    }
+    for name, ws in cases.items():
+        rc = L.mxq_quantized_matmul_ws(x, M, K, wq, sc, bi, N, 1, gs, bits, bias, y, ws, need,
+                                       None)
+        assert rc == _lib.MXQ_ERR_INVALID, name
+        assert b"overlaps" in L.mxq_last_error(), name

@@ -439,6 +439,19 @@ int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t*
   int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
                         bias, y);
   if (rc) return rc;
+  // the tiler reads the weight triple while it writes the workspace, and the kernel
+  // reads the workspace while it writes y: the workspace may share no byte with them
+  const uintptr_t w0 = reinterpret_cast<uintptr_t>(workspace), w1 = w0 + static_cast<uintptr_t>(need);
+  auto overlaps = [&](const void* p, int64_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return p && bytes > 0 && a < w1 && w0 < a + static_cast<uintptr_t>(bytes);
+  };
+  const int64_t groups = N * (K / group_size);
+  if (overlaps(x, M * K * 2) || overlaps(wq, N * K / 32 * bits * 4) ||
+      overlaps(scales, groups * 2) || overlaps(biases, groups * 2) || overlaps(bias, N * 2) ||
+      overlaps(y, M * N * 2))
+    return fail(MXQ_ERR_INVALID,
+                "[quantized_matmul] The workspace overlaps an input or the output.");
   rc = mxq_tile(wq, scales, biases, N, K, group_size, bits, workspace, stream);
   if (rc) return rc;
   return mxq_qmm_tiled(x, M, K, workspace, N, group_size, bits, bias, y, stream);
