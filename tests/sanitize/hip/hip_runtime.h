@@ -1,0 +1,49 @@
+// Host-only stand-in for the few HIP runtime pieces libmxq's host C++
+// (mxq_api.cpp, mxq_safetensors.cpp) uses, so that code builds with g++ under
+// AddressSanitizer / UndefinedBehaviorSanitizer on a machine without a GPU.
+// "Device" memory is ordinary host memory in this build: copies are memcpy,
+// pinned buffers are malloc, streams and events complete immediately. Test
+// infrastructure only (tests/test_sanitize.py); never part of libmxq.
+#pragma once
+
+#include <cstddef>
+#include <cstdlib>
+#include <cstring>
+
+#define __host__
+#define __device__
+
+typedef int hipError_t;
+enum : int { hipSuccess = 0, hipErrorInvalidValue = 1, hipErrorOutOfMemory = 2,
+             hipErrorNotSupported = 801 };
+typedef struct ihipStream_t* hipStream_t;
+typedef struct ihipEvent_t* hipEvent_t;
+enum hipMemcpyKind { hipMemcpyHostToHost = 0, hipMemcpyHostToDevice = 1 };
+#define hipHostMallocDefault 0u
+#define hipEventDisableTiming 2u
+
+inline const char* hipGetErrorString(hipError_t) { return "host-only build"; }
+inline hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
+  *p = std::malloc(n);
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipHostFree(void* p) {
+  std::free(p);
+  return hipSuccess;
+}
+inline hipError_t hipMemcpyAsync(void* dst, const void* src, size_t n, hipMemcpyKind,
+                                 hipStream_t) {
+  std::memcpy(dst, src, n);
+  return hipSuccess;
+}
+inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+inline hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) {
+  *e = reinterpret_cast<hipEvent_t>(std::malloc(1));
+  return *e ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipEventDestroy(hipEvent_t e) {
+  std::free(e);
+  return hipSuccess;
+}
+inline hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
+inline hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }

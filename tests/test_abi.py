@@ -82,6 +82,23 @@ def test_matmul_empty_is_noop(mxq_lib):
     assert _qmm(mxq_lib, N=0, x=None, y=None) == _lib.MXQ_OK
 
 
+def test_matmul_caps_k(mxq_lib):
+    # the kernels' 32-bit activation offsets (row * K * 2 for up to 256 rows) stay below
+    # 2^31 only up to K = 2^22; above, every matmul entry point refuses before launching
+    L = mxq_lib
+    f = _fake()
+    big, ok = (1 << 22) + 64, 1 << 22
+    assert _qmm(L, K=big) == _lib.MXQ_ERR_INVALID
+    assert b"2^22" in L.mxq_last_error()
+    assert _qmm(L, K=ok, M=0) == _lib.MXQ_OK
+    assert L.mxq_qmm(f, 16, big, f, f, f, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+    assert L.mxq_qmv(f, 2, big, f, f, f, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+    for fn in (L.mxq_qmm_tiled, L.mxq_qmv_tiled, L.mxq_quantized_matmul_tiled):
+        assert fn(f, 2, big, f, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+        assert b"2^22" in L.mxq_last_error()
+        assert fn(None, 0, ok, None, 64, 64, 4, None, None, None) == _lib.MXQ_OK
+
+
 def test_qmv_rejects_large_m(mxq_lib):
     L = mxq_lib
     rc = L.mxq_qmv(_fake(), 9, 256, _fake(), _fake(), _fake(), 64, 64, 4, None, _fake(), None)

@@ -78,7 +78,8 @@ def _raw(tmp_path, header, data=b"", n=None):
 
 
 @pytest.mark.parametrize("case", ["tiny", "length", "json", "range", "size", "dup", "deep",
-                                  "offsets", "missing"])
+                                  "offsets", "missing", "end_overflow", "begin_overflow",
+                                  "unknown_dtype_range", "size_overflow"])
 def test_malformed_files_are_rejected(tmp_path, case):
     ok = {"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}
     if case == "tiny":
@@ -103,6 +104,18 @@ def test_malformed_files_are_rejected(tmp_path, case):
     elif case == "offsets":
         p = _raw(tmp_path, {"a": {"dtype": "F32", "shape": [2], "data_offsets": [8, 0]}},
                  b"\0" * 8)
+    elif case == "end_overflow":  # offset + start would wrap past INT64_MAX
+        p = _raw(tmp_path, {"a": {"dtype": "U8", "shape": [64],
+                                  "data_offsets": [2 ** 63 - 101, 2 ** 63 - 37]}}, b"\0" * 8)
+    elif case == "begin_overflow":
+        p = _raw(tmp_path, {"a": {"dtype": "U8", "shape": [0],
+                                  "data_offsets": [2 ** 63 - 2, 2 ** 63 - 2]}}, b"\0" * 8)
+    elif case == "unknown_dtype_range":  # a dtype without a known size is range-checked too
+        p = _raw(tmp_path, {"a": {"dtype": "XX", "shape": [4],
+                                  "data_offsets": [0, 2 ** 63 - 10]}}, b"\0" * 8)
+    elif case == "size_overflow":  # element count x item size past INT64_MAX
+        p = _raw(tmp_path, {"a": {"dtype": "F64", "shape": [2 ** 62],
+                                  "data_offsets": [0, 8]}}, b"\0" * 8)
     else:
         p = tmp_path / "none.safetensors"
     with pytest.raises(ValueError, match=r"\[safetensors\]"):

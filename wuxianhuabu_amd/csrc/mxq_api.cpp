@@ -41,6 +41,12 @@ bool bits_supported(int bits) {
 }
 bool gs_supported(int gs) { return gs == 32 || gs == 64 || gs == 128; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+// rows x cols elements (both non-negative): their bit counts, and rows or cols
+// rounded up to a block of 64, stay within int64
+bool fits(int64_t rows, int64_t cols) {
+  return rows <= INT64_MAX / 64 && cols <= INT64_MAX / 64 &&
+         (rows == 0 || cols <= INT64_MAX / 64 / rows);
+}
 
 int check_bits_gs(const char* op, int bits, int gs, int64_t cols) {
   if (!bits_supported(bits))
@@ -85,6 +91,11 @@ namespace {
 
 bool dtype_ok(int d) { return d == MXQ_FLOAT32 || d == MXQ_BFLOAT16; }
 
+// The matmul kernels address a tile of up to 256 activation rows with 32-bit
+// byte offsets (row * K * 2) and 32-bit buffer sizes (rows * K * 2): K up to
+// 2^22 keeps both below 2^31.
+constexpr int64_t kMaxK = int64_t{1} << 22;
+
 int check_matmul(const char* op, const void* x, int64_t M, int64_t K, const uint32_t* wq,
                  const void* scales, const void* biases, int64_t N, int gs, int bits,
                  const void* bias, const void* y) {
@@ -98,6 +109,9 @@ int check_matmul(const char* op, const void* x, int64_t M, int64_t K, const uint
     return fail(MXQ_ERR_INVALID, "[%s] K must be positive (got 0).", op);
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXQ_ERR_INVALID, "[%s] Dimensions above 2^31-1 are not supported.", op);
+  if (K > kMaxK)
+    return fail(MXQ_ERR_INVALID, "[%s] K above 2^22 (%lld) is not supported (got %lld).", op,
+                static_cast<long long>(kMaxK), static_cast<long long>(K));
   if (M == 0 || N == 0) return MXQ_OK;
   if (!x || !wq || !scales || !biases || !y)
     return fail(MXQ_ERR_NULL, "[%s] x, w, scales, biases and y must be non-NULL.", op);
@@ -136,7 +150,7 @@ int mxq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_
   if (!bits_supported(bits))
     return fail(MXQ_ERR_INVALID, "[pack] The requested number of bits %d is not supported.",
                 bits);
-  if (rows < 0 || cols < 0 || (cols * bits) % 32 != 0)
+  if (rows < 0 || cols < 0 || !fits(rows, cols) || (cols * bits) % 32 != 0)
     return fail(MXQ_ERR_INVALID,
                 "[pack] cols*bits must be a non-negative multiple of 32 (rows=%lld, "
                 "cols=%lld, bits=%d).",
@@ -153,7 +167,7 @@ int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t
   if (!bits_supported(bits))
     return fail(MXQ_ERR_INVALID, "[unpack] The requested number of bits %d is not supported.",
                 bits);
-  if (rows < 0 || cols < 0 || (cols * bits) % 32 != 0)
+  if (rows < 0 || cols < 0 || !fits(rows, cols) || (cols * bits) % 32 != 0)
     return fail(MXQ_ERR_INVALID,
                 "[unpack] cols*bits must be a non-negative multiple of 32 (rows=%lld, "
                 "cols=%lld, bits=%d).",
@@ -171,6 +185,7 @@ int mxq_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int gro
   int rc = check_bits_gs("quantize", bits, group_size, cols);
   if (rc) return rc;
   if (rows < 0) return fail(MXQ_ERR_INVALID, "[quantize] rows must be non-negative.");
+  if (!fits(rows, cols)) return fail(MXQ_ERR_INVALID, "[quantize] rows x cols out of range.");
   if (!dtype_ok(w_dtype) || !dtype_ok(sb_dtype))
     return fail(MXQ_ERR_INVALID,
                 "[quantize] Only float32 and bfloat16 weights, scales and biases are "
@@ -194,6 +209,7 @@ int mxq_dequantize(const uint32_t* wq, const void* scales, const void* biases, i
   int rc = check_bits_gs("dequantize", bits, group_size, cols);
   if (rc) return rc;
   if (rows < 0) return fail(MXQ_ERR_INVALID, "[dequantize] rows must be non-negative.");
+  if (!fits(rows, cols)) return fail(MXQ_ERR_INVALID, "[dequantize] rows x cols out of range.");
   if (!dtype_ok(sb_dtype) || !dtype_ok(out_dtype))
     return fail(MXQ_ERR_INVALID,
                 "[dequantize] Only float32 and bfloat16 scales, biases and outputs are "
@@ -258,6 +274,7 @@ int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits) {
   int rc = check_bits_gs("tile", bits, group_size, K);
   if (rc) return rc;
   if (N < 0) return fail(MXQ_ERR_INVALID, "[tile] N must be non-negative.");
+  if (!fits(N, K)) return fail(MXQ_ERR_INVALID, "[tile] N x K out of range.");
   if (K % 64 != 0)
     return fail(MXQ_ERR_INVALID,
                 "[tile] The tiled layout needs K to be a multiple of 64 (got %lld).",
@@ -311,6 +328,9 @@ int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void*
                 op);
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXQ_ERR_INVALID, "[%s] Dimensions above 2^31-1 are not supported.", op);
+  if (K > kMaxK)
+    return fail(MXQ_ERR_INVALID, "[%s] K above 2^22 (%lld) is not supported (got %lld).", op,
+                static_cast<long long>(kMaxK), static_cast<long long>(K));
   if (mxq::tiled::total_bytes(N, K, gs, bits) / mxq::tiled::row_blocks(N == 0 ? 1 : N) >
       INT32_MAX)
     return fail(MXQ_ERR_INVALID, "[%s] K too large for one row block (%lld).", op,
@@ -422,7 +442,7 @@ int64_t mxq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int
   // MFMA kernels accumulate each output in the same order: the result bits are the same.
   constexpr int64_t kTileMinM = 1024;
   if (M < kTileMinM || M > INT32_MAX || N == 0 || N > INT32_MAX || K == 0 || K % 64 != 0 ||
-      K > INT32_MAX || !mxq::detail::qmm_supports_bits(bits))
+      K > kMaxK || !mxq::detail::qmm_supports_bits(bits))
     return 0;
   return mxq::tiled::total_bytes(N, K, group_size, bits);
 }
@@ -513,7 +533,9 @@ int mxq_mod_gate(const void* x, const void* other, int64_t S, int64_t hidden, co
 int mxq_rmsnorm_rope(const void* x, int64_t S, int64_t heads, int64_t head_dim,
                      const void* weight, const void* cos, const void* sin, int table_dtype,
                      int rot, float eps, void* out, mxq_stream stream) {
-  if (heads < 0) return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] Negative dimension.");
+  if (S < 0 || heads < 0) return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] Negative dimension.");
+  if (heads > INT32_MAX || (heads > 0 && S > INT64_MAX / heads))
+    return fail(MXQ_ERR_INVALID, "[rmsnorm_rope] S x heads rows out of range.");
   int rc = check_rows("rmsnorm_rope", S * heads, head_dim, {x, weight, out});
   if (rc) return rc;
   if (head_dim > 512)

@@ -200,9 +200,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   // k) ahead of the step being multiplied (g): activations (step g+2) and
   // weights (step g+3). At the last step they stop and repeat it: a repeated
   // request is harmless and keeps every step's request count equal. Plain
-  // scalars, advanced in place, so they stay in SGPRs.
+  // scalars, advanced in place, so they stay in SGPRs, as do the buffer
+  // descriptors of their current tiles (rebuilt only when a position moves on
+  // to its next tile).
   int xs_r = 0, xs_k = 0, ws_r = 0, ws_k = 0;
   int64_t xs_t = tile_of(0), ws_t = xs_t;
+  __amdgpu_buffer_rsrc_t xr_cur = x_rsrc(m0_of(xs_t)), wr_cur = w_rsrc(n0_of(ws_t));
 
   // request i of a step (activations first, needed a step sooner); st = the
   // step's ring index g mod 3: activations of step g+2 go to stage (g+2) mod 3,
@@ -416,18 +419,20 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   // One K step g (st = g mod 3; J = g & 1 selects the unpack buffers). FULL
   // steps also read step g+1's record, multiply step g and unpack step g+1;
   // the first two fill steps (g = -3, -2) only request. Requests are spread
-  // over the MFMA pairs.
+  // over the MFMA pairs. Pair q covers K slice sl = q / MB of token block
+  // mb = q % MB, so an accumulator is reused 2*MB MFMAs later (not 2).
   auto step = [&](auto Jc, auto fullc, int g, int st) __attribute__((always_inline)) {
     constexpr int J = decltype(Jc)::value;
     constexpr bool FULL = decltype(fullc)::value;
     // this step's requests: activations (none before step 0), weights
-    const __amdgpu_buffer_rsrc_t xr = x_rsrc(m0_of(xs_t)), wr = w_rsrc(n0_of(ws_t));
+    const __amdgpu_buffer_rsrc_t xr = xr_cur, wr = wr_cur;
     const int kx = xs_k, kw = ws_k;
     const bool x_on = g >= -2;
     if (x_on && ++xs_k == nk) {
       if (xs_r + 1 < my_tiles) {
         xs_k = 0;
         xs_t = tile_of(++xs_r);
+        xr_cur = x_rsrc(m0_of(xs_t));
       } else {
         xs_k = nk - 1;
       }
@@ -436,6 +441,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       if (ws_r + 1 < my_tiles) {
         ws_k = 0;
         ws_t = tile_of(++ws_r);
+        wr_cur = w_rsrc(n0_of(ws_t));
       } else {
         ws_k = nk - 1;
       }
@@ -443,9 +449,10 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
     if constexpr (FULL) {
       const uint8_t* xb = xl + st * XSTAGE;
       const uint8_t* wb = wl + (st == 2 ? 0 : st + 1) * WSTAGE + wave * R::BYTES;
+      auto fq = [](int q) { return (q % MB) * 4 + q / MB; };  // fragment of pair q
       bf16x8 f[4];
 #pragma unroll
-      for (int q = 0; q < 3; ++q) f[q] = read_frag(xb, q);
+      for (int q = 0; q < 3; ++q) f[q] = read_frag(xb, fq(q));
       RawRun<BITS> raw;
       read_raw(wb, raw);
       const float s0 = __uint_as_float(raw.sb[0] << 16);
@@ -458,8 +465,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
 #pragma unroll
         for (int i = 0; i < L; ++i)
           if (i * SLOTS / L == q) request(i, st, xr, kx, wr, kw);
-        if (q + 3 < SLOTS) f[(q + 3) % 4] = read_frag(xb, q + 3);
-        const int mb = q / 4, sl = q % 4;
+        if (q + 3 < SLOTS) f[(q + 3) % 4] = read_frag(xb, fq(q + 3));
+        const int mb = q % MB, sl = q / MB;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           const bf16x8 wv = __builtin_bit_cast(

@@ -370,16 +370,26 @@ int mxq_st_open(const char* path, mxq_safetensors** out) {
     release(st);
     return st_fail(MXQ_ERR_INVALID, "[safetensors] bad header: %s: %s", e.c_str(), path);
   }
-  const int64_t start = 8 + static_cast<int64_t>(n);
+  // data region [start, size); the parser guarantees 0 <= offset (lo) and
+  // 0 <= nbytes (hi - lo), so both comparisons below are between non-negative
+  // values no larger than the file, and no sum can overflow
+  const uint64_t start = 8 + n;
+  const uint64_t data = st->size - start;
   for (size_t i = 0; i < st->entries.size(); ++i) {
     Entry& e = st->entries[i];
-    e.offset += start;
+    const bool in_file = static_cast<uint64_t>(e.offset) <= data &&
+                         static_cast<uint64_t>(e.nbytes) <= data - static_cast<uint64_t>(e.offset);
+    if (in_file) e.offset += static_cast<int64_t>(start);
     int64_t count = 1;
-    for (int64_t d : e.shape) count = d == 0 || count <= INT64_MAX / d ? count * d : -1;
+    for (int64_t d : e.shape)  // -1 once the product overflows
+      count = count < 0 ? -1 : d == 0 || count <= INT64_MAX / d ? count * d : -1;
+    // a dtype this reader does not know is kept as raw bytes (range-checked above,
+    // element count unchecked)
     const int64_t isz = itemsize(e.dtype);
-    if (e.offset + e.nbytes > static_cast<int64_t>(st->size) ||
-        (isz && count >= 0 && count * isz != e.nbytes) || count < 0 ||
-        !st->index.emplace(e.key, i).second) {
+    int64_t want = 0;
+    const bool size_ok = count >= 0 && (isz == 0 || (!__builtin_mul_overflow(count, isz, &want) &&
+                                                      want == e.nbytes));
+    if (!in_file || !size_ok || !st->index.emplace(e.key, i).second) {
       const std::string k = e.key;
       release(st);
       return st_fail(MXQ_ERR_INVALID,
