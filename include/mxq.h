@@ -133,6 +133,22 @@ int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t*
                             int group_size, int bits, const void* bias, void* y, void* workspace,
                             size_t ws_bytes, mxq_stream stream);
 
+/* mxq_quantized_matmul_ws for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The workspace is a static device array of MXQ_NOALLOC_SCRATCH_BYTES,
+ * one per GPU, held by the library until the process ends; nothing is allocated
+ * and nothing is freed. When the tiled path applies (workspace_size > 0) and the
+ * tiled weight fits, the weight is tiled into that array and the tiled kernel runs
+ * (the same result bits as mxq_quantized_matmul); when it does not apply, this is
+ * mxq_quantized_matmul; a tiled weight above the array's size is MXQ_ERR_INVALID.
+ * Every call on one GPU shares that GPU's array: calls that may overlap on one GPU
+ * (different streams, not ordered) race and must be serialised by the caller. */
+#define MXQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int mxq_quantized_matmul_noalloc(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                                 const void* scales, const void* biases, int64_t N,
+                                 int transpose, int group_size, int bits, const void* bias,
+                                 void* y, mxq_stream stream);
+
 /* Large-M path only (bf16 MFMA, weights unpacked in registers). Any M >= 0. */
 int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
             const void* biases, int64_t N, int group_size, int bits, const void* bias,

@@ -165,6 +165,8 @@ int api(uint64_t seed, int count) {
     mxq_quantized_matmul_workspace_size(M, N, K, gs, b);
     mxq_quantized_matmul_ws(x, M, K, wq, s, c, N, 1, gs, b, nullptr, y, t,
                             static_cast<size_t>(below(1u << 20)), nullptr);
+    mxq_quantized_matmul_noalloc(x, M, K, wq, s, c, N, static_cast<int>(below(2)), gs, b,
+                                 nullptr, y, nullptr);
     mxq_qmm(x, M, K, wq, s, c, N, gs, b, nullptr, y, nullptr);
     mxq_qmv(x, M, K, wq, s, c, N, gs, b, nullptr, y, nullptr);
     mxq_tiled_bytes(N, K, gs, b);

@@ -12,6 +12,8 @@
 
 #define __host__
 #define __device__
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) (&(x))
 
 typedef int hipError_t;
 enum : int { hipSuccess = 0, hipErrorInvalidValue = 1, hipErrorOutOfMemory = 2,
@@ -47,3 +49,17 @@ inline hipError_t hipEventDestroy(hipEvent_t e) {
 }
 inline hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
 inline hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+inline hipError_t hipGetDevice(int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+inline hipError_t hipSetDevice(int) { return hipSuccess; }
+inline hipError_t hipStreamGetDevice(hipStream_t, int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+template <typename T>
+inline hipError_t hipGetSymbolAddress(void** p, const T* symbol) {
+  *p = const_cast<void*>(static_cast<const void*>(symbol));
+  return hipSuccess;
+}

@@ -25,6 +25,7 @@ MXQ_ACT_NONE = 0
 MXQ_ACT_GELU_TANH = 1
 MXQ_ACT_SWIGLU = 2
 ABI_VERSION = 1
+MXQ_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # every symbol include/mxq.h declares, with (restype, argtypes)
 _i64, _int, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
@@ -38,6 +39,8 @@ SIGNATURES = {
     "mxq_quantized_matmul_workspace_size": (_i64, [_i64, _i64, _i64, _int, _int]),
     "mxq_quantized_matmul_ws": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _int,
                                        _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mxq_quantized_matmul_noalloc": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int,
+                                            _int, _vp, _vp, _vp]),
     "mxq_qmm": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_qmv": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _int, _vp, _vp, _vp]),
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 
 #include "mxq_internal.hpp"
 #include "mxq_tiled.hpp"
@@ -475,6 +476,72 @@ int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t*
   rc = mxq_tile(wq, scales, biases, N, K, group_size, bits, workspace, stream);
   if (rc) return rc;
   return mxq_qmm_tiled(x, M, K, workspace, N, group_size, bits, bias, y, stream);
+}
+
+}  // extern "C"
+
+// ---- the matmul that allocates nothing: mxq_quantized_matmul_ws with its
+// workspace in a static device array, one per GPU (each GPU holds its copy until
+// the process ends). Host code never uses the array's name as an address: the
+// device address of each GPU's copy is looked up once, with that GPU current,
+// and kept per device.
+static __device__ __align__(256) uint8_t scratch[MXQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices];  // device address of `scratch` on each GPU (null: not looked up)
+
+// The scratch address on the device `stream` belongs to (the current device for
+// the null stream).
+int scratch_address(hipStream_t stream, void** out) {
+  int cur = 0, dev = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess) e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status("quantized_matmul", e);
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MXQ_ERR_UNSUPPORTED, "[quantized_matmul] Device %d is beyond the %d this library "
+                "keeps a scratch address for.", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return hip_status("quantized_matmul", e);
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return hip_status("quantized_matmul", e);
+    if (!p) return fail(MXQ_ERR_HIP, "[quantized_matmul] The scratch array has no device address.");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return MXQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mxq_quantized_matmul_noalloc(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                                 const void* scales, const void* biases, int64_t N,
+                                 int transpose, int group_size, int bits, const void* bias,
+                                 void* y, mxq_stream stream) {
+  const int64_t need = mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits);
+  if (need < 0) return static_cast<int>(need);
+  if (transpose != 1 || need == 0)  // no workspace used: the plain operator
+    return mxq_quantized_matmul(x, M, K, wq, scales, biases, N, transpose, group_size, bits,
+                                bias, y, stream);
+  if (need > MXQ_NOALLOC_SCRATCH_BYTES)
+    return fail(MXQ_ERR_INVALID,
+                "[quantized_matmul] The tiled weight (%lld bytes) exceeds the %lld-byte scratch "
+                "of mxq_quantized_matmul_noalloc; pass a workspace to mxq_quantized_matmul_ws.",
+                static_cast<long long>(need),
+                static_cast<long long>(MXQ_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  const int rc = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (rc) return rc;
+  return mxq_quantized_matmul_ws(x, M, K, wq, scales, biases, N, transpose, group_size, bits,
+                                 bias, y, ws, static_cast<size_t>(need), stream);
 }
 
 }  // extern "C"
