@@ -15,11 +15,15 @@ cost is reported as tile_ms and is not part of a step), and each step runs the t
 kernel. The same workloads on the MLX-layout kernels (mxq_qmm / mxq_qmv, no tiling)
 are reported beside them as qmm_mlx_layout / gemv_mlx_layout, and a dense bf16 library
 GEMM of the headline shape (torch.mm on the dequantized weight) as dense_bf16_library,
-the MFMA rate this board sustains without any unpacking. The CPU baseline (the oracle's restatement of mlx's CPU quantized
-matmul loop, timed on this host) and a sampled-row correctness check run after the
-GPU timing; they are the only part of this file that touches the oracle.
+the MFMA rate this board sustains without any unpacking. The other configurations
+(c0 M=256 K=2048 N=2048, c1 M=3600 K=4096 N=4096, the c3 down projection K=16384 N=4096
+on a GELU input, the c4 4-bit DiT block chain, and the Gemma-4 tied-logits GEMV M=1
+K=3840 N=262144) are timed too, each with its roofline fraction. The CPU baseline (the
+oracle's restatement of mlx's CPU quantized matmul loop, timed on this host) and the
+correctness checks of every configuration's sampled rows run after the GPU timing; they
+are the only part of this file that touches the oracle.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--all] [--headline-only]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--headline-only]
 """
 import argparse
 import json
@@ -68,7 +72,7 @@ def make_inputs(torch, mx, c, dev):
     x = x.bfloat16()
     g.manual_seed(2000 + c["seed"])
     w = torch.randn(c["N"], c["K"], generator=g, device=dev) * 0.02
-    wq, s, b = mx.quantized(w, c["gs"], c["bits"], scales_dtype=torch.bfloat16)
+    wq, s, b = mx.quantized(w, c["gs"], c["bits"], mode="minmax", scales_dtype=torch.bfloat16)
     del w
     return x, wq, s, b
 
@@ -117,6 +121,11 @@ def time_graph(torch, fn, launches, replays, rotate=1):
     return per, ev[0].elapsed_time(ev[replays])
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
+                  "this workload in separate runs, scaled by a 1 GiB copy kernel; not "
+                  "measured in this run")
+
+
 def load_traffic(kernel_key):
     """Memory-side bytes per launch of one kernel, measured with rocprofv3 --pmc
     (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy
@@ -130,7 +139,17 @@ def load_traffic(kernel_key):
         return None
 
 
-def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
+def check_rows(M, n=256, seed=7):
+    """Rows of a large-M output checked against the oracle: n seeded rows, the last
+    row, and the rows either side of the 256-row / remainder launch seam."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    seam = (M // 256) * 256
+    extra = [M - 1] + ([seam - 1, seam] if 0 < seam < M else [])
+    return np.unique(np.concatenate([rng.choice(M, min(n, M), replace=False), extra]))
+
+
+def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s, checks=()):
     """The oracle, as checker and as the CPU baseline (this host's cores)."""
     import numpy as np
     from oracle import pyoracle as O
@@ -145,9 +164,7 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
     out = {}
     # -- correctness on sampled rows (qmm) and on the full GEMV output --
     x, wq, s, b, y = bufs["qmm"]
-    rng = np.random.default_rng(7)
-    rows = np.unique(np.concatenate([rng.choice(qmm_c["M"], 24, replace=False),
-                                     [qmm_c["M"] - 1]]))
+    rows = check_rows(qmm_c["M"])
     xh = host_u16(x)
     wqh, sh, bh = host_u32(wq), host_u16(s), host_u16(b)
     yg = y.float()[torch.as_tensor(rows, device=y.device)].cpu().numpy().astype(np.float64)
@@ -155,12 +172,24 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
     ref_w = O.qmm_f64_bf16w(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], rows=rows,
                             threads=threads)
     ref = O.qmm_f64(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], rows=rows, threads=threads)
+    # the oracle's restatement of mlx's CPU quantized matmul (bf16 products and running
+    # sum) on the first rows of the sample: how far the reference's CPU backend, as
+    # restated, sits from the kernel and from the exact result
+    prow = rows[:24]
+    port = O.bf16_to_f32(O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0,
+                                        rows=prow, threads=threads)).astype(np.float64)
+    sub = np.searchsorted(rows, prow)
     out["qmm_check"] = {
         "rows": int(len(rows)),
+        "rows_note": "256 seeded rows, the last row, and rows 14335/14336 either side of "
+                     "the 256-row / 64-row launch seam",
         "max_rel_vs_exact": float(np.abs(yg - ref).max() / np.abs(ref).max()),
         "max_rel_vs_bf16w": float(np.abs(yg - ref_w).max() / np.abs(ref_w).max()),
         "cosine": float((yg.ravel() @ ref.ravel()) /
                         (np.linalg.norm(yg) * np.linalg.norm(ref))),
+        "max_rel_vs_mlx_cpu_port": float(np.abs(yg[sub] - port).max() / np.abs(port).max()),
+        "mlx_cpu_port_vs_exact": float(np.abs(port - ref[sub]).max() / np.abs(ref[sub]).max()),
+        "mlx_cpu_port_rows": int(len(prow)),
     }
     out["qmm_check"]["pass"] = out["qmm_check"]["max_rel_vs_exact"] <= 2e-2
     gx, gwq, gs_, gb, gy = bufs["gemv"]
@@ -172,6 +201,23 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s):
     for k in ("qmm_check", "gemv_check"):
         if not out[k]["pass"]:
             print(f"[bench] {k} FAILED: {out[k]}", file=sys.stderr, flush=True)
+    # the other configurations: their sampled rows against the fp64 oracle, exact weights
+    # (the north-star metric) and weights rounded to bf16 as the MFMA kernel takes them
+    extra_checks = {}
+    for c in checks:
+        r_exact = O.qmm_f64(c["x"], c["wq"], c["s"], c["b"], c["gs"], c["bits"], threads=threads)
+        r_w = O.qmm_f64_bf16w(c["x"], c["wq"], c["s"], c["b"], c["gs"], c["bits"],
+                              threads=threads)
+        rel = float(np.abs(c["y"] - r_exact).max() / np.abs(r_exact).max())
+        extra_checks[c["name"]] = {
+            "rows": int(len(c["rows"])), "max_rel_vs_exact": rel,
+            "max_rel_vs_bf16w": float(np.abs(c["y"] - r_w).max() / np.abs(r_w).max()),
+            "pass": rel <= 2e-2}
+        if not extra_checks[c["name"]]["pass"]:
+            print(f"[bench] check FAILED: {c['name']}: {extra_checks[c['name']]}",
+                  file=sys.stderr, flush=True)
+    if checks:
+        out["extra_checks"] = extra_checks
 
     # -- CPU baseline: mlx CPU qmm loop structure, bf16 arithmetic, 1 core --
     K, N = qmm_c["K"], qmm_c["N"]
@@ -314,7 +360,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip oracle check and CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
-    ap.add_argument("--all", action="store_true", help="also time c0, c1, c3-down, c4 chain")
+    ap.add_argument("--all", action="store_true",
+                    help="accepted for compatibility: c0, c1, c3-down, the c4 chain and the "
+                         "Gemma-4 logits GEMV are timed by default")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the tiled qmm and GEMV (what the rocprof summaries trace)")
     ap.add_argument("--calibrate", action="store_true",
@@ -328,6 +376,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    import numpy as np
     import torch
     import wuxianhuabu_amd as mx
 
@@ -545,12 +594,29 @@ def main():
                    "bytes_per_launch": gbytes},
         "roofline": {"bound": "hbm", "achieved": gemv_gbs, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": gemv_gbs / HBM_PEAK_GBS,
-                     "traffic": load_traffic("qmv_tiled 6-bit M=2 K=4096 N=24576")},
+                     "traffic": load_traffic("qmv_tiled 6-bit M=2 K=4096 N=24576"),
+                     "traffic_source": TRAFFIC_SOURCE},
     }
 
-    # ---------------- optional extra configs ----------------
-    if args.all:
+    # ---------------- the other configurations ----------------
+    checks = []  # sampled outputs checked against the oracle in the CPU leg
+    if not args.headline_only:
         extra = {}
+
+        def host_rows(t, rows):
+            return t[torch.as_tensor(rows, device=t.device)].float().cpu().numpy().astype(
+                np.float64)
+
+        def keep_check(name, cx, cwq, cs, cb, cy, gs, bits, rows):
+            checks.append(dict(
+                name=name, rows=rows, gs=gs, bits=bits,
+                x=cx[torch.as_tensor(rows, device=cx.device)].contiguous().view(torch.int16)
+                  .cpu().numpy().view(np.uint16),
+                wq=cwq.contiguous().view(torch.int32).cpu().numpy().view(np.uint32),
+                s=cs.contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
+                b=cb.contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
+                y=host_rows(cy, rows)))
+
         # weights resident in the tiled layout (tiled once, at load), as in the headline;
         # 20 launches per HIP graph so that host launch gaps do not count
         def qmm_call(cx, ctw, cy):
@@ -561,28 +627,34 @@ def main():
             ex, ewq, es, eb = make_inputs(torch, mx, e, dev)
             etw = mx.tile(ewq, es, eb, e["gs"], e["bits"])
             ey = torch.empty(e["M"], e["N"], dtype=torch.bfloat16, device=dev)
-            del ewq, es, eb
             p, t = time_graph(torch, lambda _i, ex=ex, etw=etw, ey=ey: qmm_call(ex, etw, ey),
                               20, max(5, steps // 3))
             a = sum(p) / len(p)
-            extra[e["name"]] = {"ms": a, "tflops": 2.0 * e["M"] * e["N"] * e["K"] / a / 1e9}
-            del ex, etw, ey
+            tf = 2.0 * e["M"] * e["N"] * e["K"] / a / 1e9
+            extra[e["name"]] = {"ms": a, "tflops": tf,
+                                "roofline": {"bound": "mfma", "frac": tf / BF16_PEAK_TFLOPS}}
+            keep_check(e["name"], ex, ewq, es, eb, ey, e["gs"], e["bits"],
+                       np.arange(e["M"]) if e["M"] <= 256 else check_rows(e["M"], 64))
+            del ex, ewq, es, eb, etw, ey
         chain = []
         for i, (nm, M, K, N) in enumerate(C4_CHAIN):
             cc = dict(M=M, K=K, N=N, gs=64, bits=4, seed=40 + i)
             cx, cwq, cs, cb = make_inputs(torch, mx, cc, dev)
-            chain.append((cx, mx.tile(cwq, cs, cb, 64, 4),
+            chain.append((nm, cx, (cwq, cs, cb), mx.tile(cwq, cs, cb, 64, 4),
                           torch.empty(M, N, dtype=torch.bfloat16, device=dev)))
-            del cwq, cs, cb
 
         def run_chain(_i):
-            for cx, ctw, cy in chain:
+            for _nm, cx, _w, ctw, cy in chain:
                 qmm_call(cx, ctw, cy)
 
         p, t = time_graph(torch, run_chain, 5, max(5, steps // 3))
         a = sum(p) / len(p)
         fl = sum(2.0 * M * N * K for _, M, K, N in C4_CHAIN)
-        extra["c4 4-bit DiT block chain"] = {"ms": a, "tflops": fl / a / 1e9}
+        extra["c4 4-bit DiT block chain"] = {
+            "ms": a, "tflops": fl / a / 1e9,
+            "roofline": {"bound": "mfma", "frac": fl / a / 1e9 / BF16_PEAK_TFLOPS}}
+        for nm, cx, (cwq, cs, cb), _ctw, cy in chain:
+            keep_check(f"c4 {nm}", cx, cwq, cs, cb, cy, 64, 4, check_rows(cx.shape[0], 16))
         del chain
         # Gemma-4 tied-embedding logits (`gemma4文本-(ltx专属).swift:306-312`): M = 1,
         # K = 3840, N = 262144, 4-bit gs64: 566 MB per token, above the 256 MB Infinity
@@ -602,11 +674,15 @@ def main():
             ok(L.mxq_qmv(P(lx), 1, lg["K"], P(lwq), P(ls_), P(lb), lg["N"], lg["gs"], lg["bits"],
                          None, P(ly), cur()))
 
-        for nm, fn in (("tiled", logits_tiled), ("MLX layout", logits_mlx)):
+        for nm, fn in (("MLX layout", logits_mlx), ("tiled", logits_tiled)):
             p, t = time_graph(torch, fn, 20, max(5, steps // 3))
             a = sum(p) / len(p)
+            gbs = lbytes / (a * 1e-3) / 1e9
             extra[f"gemma4 logits GEMV 4-bit M=1 K=3840 N=262144, {nm}"] = {
-                "us": a * 1e3, "gbs": lbytes / (a * 1e-3) / 1e9, "bytes": lbytes}
+                "us": a * 1e3, "gbs": gbs, "bytes": lbytes,
+                "roofline": {"bound": "hbm", "frac": gbs / HBM_PEAK_GBS}}
+        keep_check("gemma4 logits (tiled GEMV)", lx, lwq, ls_, lb, ly, lg["gs"], lg["bits"],
+                   np.arange(1))
         del lx, lwq, ls_, lb, ltw, ly
         res["extra"] = extra
 
@@ -615,7 +691,7 @@ def main():
         qmm_launch(0)  # the check reads the plain qmm output of the headline call
         torch.cuda.synchronize()
         cpu_leg(res, {"qmm": (x, wq, s, b, y), "gemv": (gx, gwq, gs_, gb, gy)}, QMM, GEMV,
-                args.cpu_budget)
+                args.cpu_budget, checks)
 
     line = {
         "metric": "6-bit qmm TFLOP/s (M=14400, 4096->16384) + GEMV GB/s at M=2",
@@ -636,6 +712,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
                      "traffic": load_traffic("qmm_tiled 6-bit M=14400 K=4096 N=16384"),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "kernel_avg_ms": avg_ms, "kernel_median_ms": med_ms},
     }
     line.update(res)

@@ -1,10 +1,12 @@
 """The benchmark configurations at their full sizes, on both weight layouts.
 
 c0  6-bit  M=256   K=2048  N=2048   every output row checked
-c1  6-bit  M=3600  K=4096  N=4096   sampled rows
+c1  6-bit  M=3600  K=4096  N=4096   256 sampled rows + the last row + the launch seam
 c2  6-bit  M=2     K=4096  N=24576  (GEMV) every output checked
-c3  6-bit  M=14400 K=4096  N=16384 (up) and K=16384 N=4096 on GELU_tanh(h) (down), sampled rows
-c4  4-bit  one DiT block's linear chain at M=14400 (kv at M=512), weights resident, sampled rows
+c3  6-bit  M=14400 K=4096  N=16384 (up) and K=16384 N=4096 on GELU_tanh(h) (down), 256 sampled
+    rows + the last row + rows 14335/14336 (the 256-row / 64-row launch seam)
+c4  4-bit  one DiT block's linear chain at M=14400 (kv at M=512), weights resident, 128
+    sampled rows per layer + the last row + the seam
 
 Inputs are seeded on the GPU (x from seed 1000+c, W from 2000+c, W2 from 3000+c),
 weights are quantized by the GPU quantizer (bit-exact with the oracle, see
@@ -29,7 +31,7 @@ def _weights(dev, N, K, seed, bits, gs=64):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     w = torch.randn(N, K, generator=g, device=dev) * 0.02
-    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16)
+    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16, mode="minmax")
     return wq, s, b
 
 
@@ -43,10 +45,14 @@ def _acts(dev, M, K, seed, gelu=False):
 
 
 def _rows(M, n, seed):
+    """n seeded rows, the last row and the rows either side of the seam between the
+    256-row tiles and the remainder (a second launch of 64- or 128-row tiles)."""
     if M <= n:
         return np.arange(M)
     rng = np.random.default_rng(seed)
-    return np.unique(np.concatenate([rng.choice(M, n - 1, replace=False), [M - 1]]))
+    seam = (M // 256) * 256
+    extra = [M - 1] + ([seam - 1, seam] if 0 < seam < M else [])
+    return np.unique(np.concatenate([rng.choice(M, n, replace=False), extra]))
 
 
 def _check(O, x, wq, s, b, y, rows, gs, bits, what, exact_only=False):
@@ -83,7 +89,7 @@ def test_c0(dev, O):
 
 
 def test_c1(dev, O):
-    _both_layouts(dev, O, 3600, 4096, 4096, 6, 1001, 2001, 48, "c1")
+    _both_layouts(dev, O, 3600, 4096, 4096, 6, 1001, 2001, 256, "c1")
 
 
 def test_c2_gemv(dev, O):
@@ -91,11 +97,11 @@ def test_c2_gemv(dev, O):
 
 
 def test_c3_up(dev, O):
-    _both_layouts(dev, O, 14400, 4096, 16384, 6, 1003, 2003, 32, "c3 up")
+    _both_layouts(dev, O, 14400, 4096, 16384, 6, 1003, 2003, 256, "c3 up")
 
 
 def test_c3_down_on_gelu(dev, O):
-    _both_layouts(dev, O, 14400, 16384, 4096, 6, 1003, 3003, 24, "c3 down", gelu=True)
+    _both_layouts(dev, O, 14400, 16384, 4096, 6, 1003, 3003, 256, "c3 down", gelu=True)
 
 
 def test_c4_chain_4bit(dev, O):
@@ -112,4 +118,4 @@ def test_c4_chain_4bit(dev, O):
         y_mlx = mx.quantized_matmul(x, wq, s, b, group_size=64, bits=4, path="qmm")
         y_t = mx.tiled_matmul(x, tw)
         assert torch.equal(y_mlx, y_t), f"c4 {name}: layouts differ"
-        _check(O, x, wq, s, b, y_t, _rows(M, 16, 1004 + i), 64, 4, f"c4 {name}")
+        _check(O, x, wq, s, b, y_t, _rows(M, 128, 1004 + i), 64, 4, f"c4 {name}")

@@ -68,7 +68,7 @@ def test_fused_matches_unfused_chain(dev, O):
     x = torch.randn(M, K, generator=g, device=dev).bfloat16()
     w = torch.randn(2 * F, K, generator=g, device=dev) * 0.02
     bias = (torch.randn(2 * F, generator=g, device=dev) * 0.1).bfloat16()
-    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16)
+    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16, mode="minmax")
     plain = mx.tiled_matmul(x, mx.tile(wq, s, b, gs, bits), bias=bias).float()
     gelu = mx.tiled_matmul(x, mx.tile(wq, s, b, gs, bits), bias=bias, activation="gelu_tanh")
     ref = torch.nn.functional.gelu(plain, approximate="tanh")
@@ -123,7 +123,7 @@ def test_h3_mlp_module(dev):
     tensors = {}
     for name, n, k in (("mlp.fc1", 2 * ffn, hidden), ("mlp.fc2", hidden, ffn)):
         w = torch.randn(n, k, generator=g, device=dev) * 0.05
-        wq, s, b = mx.quantized(w, 64, 6, scales_dtype=torch.bfloat16)
+        wq, s, b = mx.quantized(w, 64, 6, scales_dtype=torch.bfloat16, mode="minmax")
         tensors[name + ".weight"], tensors[name + ".scales"], tensors[name + ".biases"] = wq, s, b
         tensors[name + ".bias"] = (torch.randn(n, generator=g, device=dev) * 0.1).bfloat16()
     mlp = mx.H3MlpW.load(tensors, "mlp", hidden, ffn)

@@ -83,6 +83,23 @@ def test_quantize_bit_exact(dev, O, bits, gs, mode):
     assert np.array_equal(host_bf16(b), ref_b["biases_bf16"])
 
 
+def test_quantized_defaults_to_mlx_edge(dev, O):
+    """The drop-in quantized(w, groupSize:, bits:) uses mlx's quantizer unless told
+    otherwise (the reference's checkpoints come from mx.quantize,
+    `model/minimax h3/tools/quantize_h3_g64.py:132`), and so does
+    QuantizedLinear.from_linear."""
+    N, K = 16, 256
+    w = O.normal_f32(77, N * K, 0.0, 0.02).reshape(N, K)
+    ref = O.quantize(w, 64, 6, mode=1)
+    wq, s, b = mx.quantized(dev_f32(w, dev), 64, 6, scales_dtype=torch.bfloat16)
+    assert np.array_equal(host_words(wq), ref["wq"])
+    assert np.array_equal(host_bf16(s), ref["scales_bf16"])
+    assert np.array_equal(host_bf16(b), ref["biases_bf16"])
+    lin = mx.QuantizedLinear.from_linear(dev_f32(w, dev).bfloat16(), group_size=64, bits=6)
+    ref_b = O.quantize(O.bf16_to_f32(O.bf16_rne(w)), 64, 6, mode=1)
+    assert np.array_equal(host_words(lin.weight), ref_b["wq"])
+
+
 def test_quantize_golden(dev, golden):
     for c in golden["quantize"]:
         w = np.array(c["w"], np.float32).reshape(c["N"], c["K"])
@@ -96,7 +113,7 @@ def test_quantize_golden(dev, golden):
 
 def test_quantize_leading_dims_and_errors(dev, O):
     w = O.normal_f32(3, 2 * 3 * 128, 0, 0.02).reshape(2, 3, 128)
-    wq, s, b = mx.quantized(dev_f32(w, dev), 64, 4)
+    wq, s, b = mx.quantized(dev_f32(w, dev), 64, 4, mode="minmax")
     assert tuple(wq.shape) == (2, 3, 16) and tuple(s.shape) == (2, 3, 2)
     ref = O.quantize(w.reshape(6, 128), 64, 4)
     assert np.array_equal(host_words(wq).reshape(6, 16), ref["wq"])
@@ -128,7 +145,7 @@ def test_dequantize_bit_exact(dev, O, bits, gs):
 def test_dequantize_fp32_scales(dev, O):
     N, K, gs, bits = 4, 256, 64, 6
     w = O.normal_f32(77, N * K, 0, 0.02).reshape(N, K)
-    wq, s, b = mx.quantized(dev_f32(w, dev), gs, bits)  # fp32 scales/biases
+    wq, s, b = mx.quantized(dev_f32(w, dev), gs, bits, mode="minmax")  # fp32 scales/biases
     out = mx.dequantized(wq, s, b, gs, bits)
     assert out.dtype == torch.float32
     q = O.quantize(w, gs, bits)
@@ -143,7 +160,7 @@ def test_quantize_dequantize_round_trip_error(dev, O):
     """Size-independent property at a full config size: |w - deq(q(w))| <= s/2."""
     N, K, gs, bits = 16384, 4096, 64, 6
     w = torch.randn(N, K, device=dev, generator=torch.Generator(device=dev).manual_seed(2003)) * 0.02
-    wq, s, b = mx.quantized(w, gs, bits)
+    wq, s, b = mx.quantized(w, gs, bits, mode="minmax")
     deq = mx.dequantized(wq, s, b, gs, bits)
     err = (w - deq).abs().view(N, K // gs, gs)
     assert bool((err <= s.abs().unsqueeze(-1) / 2 * (1 + 1e-5) + 1e-7).all())

@@ -67,7 +67,7 @@ def test_mflinear_lora_matches_unfused(dev):
     g.manual_seed(9)
     K, N, M = 512, 384, 200
     w = torch.randn(N, K, generator=g, device=dev) * 0.05
-    wq, s, b = mx.quantized(w, 64, 4, scales_dtype=torch.bfloat16)
+    wq, s, b = mx.quantized(w, 64, 4, scales_dtype=torch.bfloat16, mode="minmax")
     t = {"l.weight": wq, "l.scales": s, "l.biases": b,
          "l.bias": (torch.randn(N, generator=g, device=dev) * 0.1).bfloat16()}
     fused = mx.MfLinear.load(t, "l", K).set_lora(_adapters(dev, K, N, [16, 8], 5))
@@ -87,7 +87,7 @@ def test_h3_mlp_with_fc1_lora(dev):
     t = {}
     for name, n, k in (("m.fc1", 2 * ffn, hidden), ("m.fc2", hidden, ffn)):
         wq, s, b = mx.quantized(torch.randn(n, k, generator=g, device=dev) * 0.05, 64, 6,
-                                scales_dtype=torch.bfloat16)
+                                scales_dtype=torch.bfloat16, mode="minmax")
         t[name + ".weight"], t[name + ".scales"], t[name + ".biases"] = wq, s, b
     mlp = mx.H3MlpW.load(t, "m", hidden, ffn)
     mlp.fc1.set_lora(_adapters(dev, hidden, 2 * ffn, [32], 1))

@@ -182,7 +182,7 @@ def test_quantized_linear_module(dev, O):
     w = O.normal_f32(44, N * K, 0, 0.02).reshape(N, K)
     bias = O.bf16_rne(O.normal_f32(45, N, 0, 0.1))
     lin = mx.QuantizedLinear.from_linear(torch.from_numpy(w).to(dev), bias=dev_bf16(bias, dev),
-                                         group_size=64, bits=6)
+                                         group_size=64, bits=6, mode="minmax")
     assert lin.shape == (N, K)
     q = O.quantize(w, 64, 6)
     for M in (2, 50):

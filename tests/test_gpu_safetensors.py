@@ -41,7 +41,7 @@ def test_modules_load_from_file(dev, tmp_path):
     tensors = {}
     for name, n, k in (("blk.mlp.fc1", 2 * ffn, hidden), ("blk.mlp.fc2", hidden, ffn)):
         w = torch.randn(n, k, generator=g, device=dev) * 0.05
-        wq, s, b = mx.quantized(w, 64, 6, scales_dtype=torch.bfloat16)
+        wq, s, b = mx.quantized(w, 64, 6, scales_dtype=torch.bfloat16, mode="minmax")
         tensors[name + ".weight"] = wq
         tensors[name + ".weight.scales"] = s   # the H3 spelling
         tensors[name + ".weight.biases"] = b

@@ -89,7 +89,7 @@ def test_tiled_qmm_several_tiles_per_workgroup(dev, O, bits, gs, K, M, N):
     x = torch.randn(M, K, generator=g, device=dev).bfloat16()
     w = torch.randn(N, K, generator=g, device=dev) * 0.02
     bias = (torch.randn(N, generator=g, device=dev) * 0.1).bfloat16()
-    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16)
+    wq, s, b = mx.quantized(w, gs, bits, scales_dtype=torch.bfloat16, mode="minmax")
     y_t = mx.tiled_matmul(x, mx.tile(wq, s, b, gs, bits), bias=bias, path="qmm")
     y_m = mx.quantized_matmul(x, wq, s, b, group_size=gs, bits=bits, bias=bias, path="qmm")
     assert torch.equal(y_t, y_m), f"bits={bits} gs={gs} K={K}: tiled and MLX-layout differ"

@@ -270,6 +270,36 @@ def test_mlx_cpu_restatement_close_to_exact(O):
     assert np.abs(r2 - ref).max() / scale < 5e-3
 
 
+def _one_row(O, codes, s_bf16, b_bf16, x_bf16, gs, bits):
+    K = len(codes)
+    wq = O.pack_words(np.array(codes, np.uint8).reshape(1, K), bits)
+    s = np.full((1, K // gs), s_bf16, np.uint16)
+    b = np.full((1, K // gs), b_bf16, np.uint16)
+    x = np.array(x_bf16, np.uint16).reshape(1, K)
+    return [int(O.qmm_mlx_cpu(x, wq, s, b, gs, bits, accum=a)[0, 0]) for a in (0, 1)]
+
+
+def test_mlx_cpu_restatement_accumulates_in_bf16(O):
+    """x = 1, s = 1, b = 0, q = 1, K = 512: a bf16 running sum reaches 256 and stays
+    there (256 + 1 is a tie between 256 and 258 and rounds to the even 256); an fp32
+    sum reaches 512. An fp32-accumulating restatement fails the first assertion."""
+    one = 0x3F80
+    bf, f32 = _one_row(O, [1] * 512, one, 0, [one] * 512, 64, 6)
+    assert bf == 0x4380  # 256.0
+    assert f32 == 0x4400  # 512.0
+
+
+def test_mlx_cpu_restatement_rounds_scale_times_code_first(O):
+    """w = bf16(bf16(s * q) + b): with s = 1 + 2^-7, q = 3, b = -3, s*q = 3.0234375 is a
+    tie that rounds to 3.03125, so w = 0.03125; one rounding of s*q + b gives
+    0.0234375 (exact in bf16). x = [1, 0, 0, ...] picks w_0 as the output."""
+    codes = [3] + [0] * 63
+    x = [0x3F80] + [0] * 63
+    bf, f32 = _one_row(O, codes, 0x3F81, 0xC040, x, 64, 6)
+    assert bf == 0x3D00  # 0.03125
+    assert f32 == 0x3CC0  # 0.0234375
+
+
 def test_gelu_tanh_closed_form(O):
     xs = np.array([0.0, 1.0, -1.0, 3.0, -3.0], np.float32)
     got = O.bf16_to_f32(O.gelu_tanh_bf16(O.bf16_rne(xs)))

@@ -68,7 +68,7 @@ class QuantizedLinear:
         return obj
 
     @classmethod
-    def from_linear(cls, weight, bias=None, group_size=64, bits=4, mode="minmax"):
+    def from_linear(cls, weight, bias=None, group_size=64, bits=4, mode="mlx_edge"):
         """Quantize a dense [out, in] weight (MLXNN QuantizedLinear.from(linear:))."""
         wq, s, b = ops.quantized(weight.contiguous(), group_size, bits, mode=mode)
         return cls.from_weights(wq, s, b, bias, group_size, bits)

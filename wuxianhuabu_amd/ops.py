@@ -70,14 +70,15 @@ def _as_words(w):
     raise ValueError(f"packed weights must be uint32 (got {w.dtype}).")
 
 
-def quantized(w, group_size=64, bits=4, *, mode="minmax", scales_dtype=None):
+def quantized(w, group_size=64, bits=4, *, mode="mlx_edge", scales_dtype=None):
     """Quantize w [..., K] along its last axis -> (wq uint32, scales, biases).
 
     scales/biases have w's dtype (float32 or bfloat16; `scales_dtype` overrides)
     and shape [..., K/group_size]; wq has shape [..., K*bits/32]. Codes come
     from the fp32 scale and bias, which are then rounded to the stored dtype.
-    mode "minmax": scale=(max-min)/(2^bits-1), bias=min; mode "mlx_edge":
-    mlx's sign-aware edge quantizer.
+    mode "mlx_edge" (the default, as mlx's quantize): the sign-aware edge quantizer,
+    the group's larger-magnitude extreme on code 0 exactly; mode "minmax":
+    scale=(max-min)/(2^bits-1), bias=min (the recipe of the benchmark workloads).
     """
     _check_bits_gs("quantize", bits, group_size)
     if w.ndim < 2:
