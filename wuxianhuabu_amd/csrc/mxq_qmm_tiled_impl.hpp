@@ -348,7 +348,10 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
           if (m < M) {
             uint16_t* dst = y + static_cast<int64_t>(m) * ncol + n;
             if (vec && (reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
-              *reinterpret_cast<u32x4*>(dst) = u32x4{v.x, v.y, v.z, v.w};
+              // non-temporal: the output is not read again by this kernel, and all
+              // workgroups store their tiles at about the same time, so keeping these
+              // lines out of L2 leaves it to the operands of the next tiles
+              __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
             } else {
               const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
