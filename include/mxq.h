@@ -208,6 +208,17 @@ int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_
 int mxq_tile_swiglu(const uint32_t* wq, const void* scales, const void* biases, int64_t N,
                     int64_t K, int group_size, int bits, void* tiled, mxq_stream stream);
 
+/* Tiled layout -> MLX layout (wq [N, K*bits/32], bf16 scales and biases [N, K/gs]),
+ * the inverse of mxq_tile / mxq_tile_swiglu: the same bits come back. For holders
+ * that keep only the tiled copy resident and rebuild the triple when it is asked
+ * for: the reference's QuantizedLinear parameters weight / scales / biases
+ * (`model/3模块/ltx2.5专属/ltx主干-(ltx专属).swift:177-188`) and MfLinear's
+ * dequantizedWeight() (`model/minimax h3/H3Common.swift:382-401`). */
+int mxq_untile(const void* tiled, int64_t N, int64_t K, int group_size, int bits, uint32_t* wq,
+               void* scales, void* biases, mxq_stream stream);
+int mxq_untile_swiglu(const void* tiled, int64_t N, int64_t K, int group_size, int bits,
+                      uint32_t* wq, void* scales, void* biases, mxq_stream stream);
+
 /* y = act(x * W^T + bias) on the MFMA kernel, any M >= 0:
  *   MXQ_ACT_NONE       as mxq_qmm_tiled;
  *   MXQ_ACT_GELU_TANH  weights from mxq_tile; y [M, N]. Replaces

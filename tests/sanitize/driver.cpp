@@ -172,6 +172,8 @@ int api(uint64_t seed, int count) {
     mxq_tiled_bytes(N, K, gs, b);
     mxq_tile(wq, s, c, N, K, gs, b, t, nullptr);
     mxq_tile_swiglu(wq, s, c, N, K, gs, b, t, nullptr);
+    mxq_untile(t, N, K, gs, b, static_cast<uint32_t*>(w), s, c, nullptr);
+    mxq_untile_swiglu(t, N, K, gs, b, static_cast<uint32_t*>(w), s, c, nullptr);
     mxq_quantized_matmul_tiled(x, M, K, t, N, gs, b, nullptr, y, nullptr);
     mxq_qmm_tiled(x, M, K, t, N, gs, b, nullptr, y, nullptr);
     mxq_qmv_tiled(x, M, K, t, N, gs, b, nullptr, y, nullptr);

@@ -30,6 +30,10 @@ hipError_t launch_tile(const uint32_t*, const uint16_t*, const uint16_t*, int64_
                        int, bool, void*, hipStream_t) {
   return count();
 }
+hipError_t launch_untile(const void*, int64_t, int64_t, int, int, bool, uint32_t*, uint16_t*,
+                         uint16_t*, hipStream_t) {
+  return count();
+}
 hipError_t launch_qmv(const uint16_t*, int, int, const uint32_t*, const uint16_t*,
                       const uint16_t*, int, int, int, const uint16_t*, uint16_t*, hipStream_t) {
   return count();

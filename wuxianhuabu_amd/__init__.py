@@ -17,12 +17,14 @@ from .blockops import (build_row_mod_map, fused_mod_gate, fused_norm_modscale,  
                        fused_norm_modscale_row, fused_rmsnorm_rope)
 from .ops import (LoraAdapters, TiledWeight, dequantized, pack, quantized,  # noqa: F401
                   quantized_matmul,
-                  quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack)
+                  quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack,
+                  untile)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
 
 __all__ = [
     "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
-    "pack", "unpack", "tile", "tiled_matmul", "tiled_supported", "TiledWeight", "LoraAdapters",
+    "pack", "unpack", "tile", "untile", "tiled_matmul", "tiled_supported", "TiledWeight",
+    "LoraAdapters",
     "QuantizedLinear", "MfLinear", "LTXFFN", "H3MlpW", "SafetensorsFile", "get_quantized",
     "infer_geometry", "header_candidates", "lib", "LIB_PATH", "MXQError",
     "fused_norm_modscale", "fused_norm_modscale_row", "fused_mod_gate", "fused_rmsnorm_rope",

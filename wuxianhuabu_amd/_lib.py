@@ -46,6 +46,8 @@ SIGNATURES = {
     "mxq_tiled_bytes": (_i64, [_i64, _i64, _int, _int]),
     "mxq_tile": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
     "mxq_tile_swiglu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
+    "mxq_untile": (_int, [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp]),
+    "mxq_untile_swiglu": (_int, [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp]),
     "mxq_norm_modscale": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, ctypes.c_float,
                                  _vp, _vp]),
     "mxq_mod_gate": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),

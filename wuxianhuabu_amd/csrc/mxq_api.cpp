@@ -318,6 +318,39 @@ int mxq_tile_swiglu(const uint32_t* wq, const void* scales, const void* biases, 
 }
 
 namespace {
+int untile_impl(const void* tiled, int64_t N, int64_t K, int group_size, int bits, bool pairs,
+                uint32_t* wq, void* scales, void* biases, mxq_stream stream) {
+  const int64_t bytes = mxq_tiled_bytes(N, K, group_size, bits);
+  if (bytes < 0) return static_cast<int>(bytes);
+  if (pairs && N % 2 != 0)
+    return fail(MXQ_ERR_INVALID,
+                "[untile] A SwiGLU weight has an even number of rows (got %lld).",
+                static_cast<long long>(N));
+  if (N == 0 || K == 0) return ok();
+  if (!wq || !scales || !biases || !tiled)
+    return fail(MXQ_ERR_NULL, "[untile] tiled, w, scales and biases must be non-NULL.");
+  if (!aligned4(wq) || !aligned4(scales) || !aligned4(biases) ||
+      (reinterpret_cast<uintptr_t>(tiled) & 15u) != 0)
+    return fail(MXQ_ERR_ALIGNMENT,
+                "[untile] w, scales and biases must be 4-byte aligned, tiled 16-byte aligned.");
+  return hip_status("untile", mxq::detail::launch_untile(
+                                  tiled, N, K, group_size, bits, pairs, wq,
+                                  static_cast<uint16_t*>(scales), static_cast<uint16_t*>(biases),
+                                  static_cast<hipStream_t>(stream)));
+}
+}  // namespace
+
+int mxq_untile(const void* tiled, int64_t N, int64_t K, int group_size, int bits, uint32_t* wq,
+               void* scales, void* biases, mxq_stream stream) {
+  return untile_impl(tiled, N, K, group_size, bits, false, wq, scales, biases, stream);
+}
+
+int mxq_untile_swiglu(const void* tiled, int64_t N, int64_t K, int group_size, int bits,
+                      uint32_t* wq, void* scales, void* biases, mxq_stream stream) {
+  return untile_impl(tiled, N, K, group_size, bits, true, wq, scales, biases, stream);
+}
+
+namespace {
 int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void* tiled,
                 int64_t N, int gs, int bits, const void* bias, const void* y) {
   if (M < 0 || N < 0 || K < 0)

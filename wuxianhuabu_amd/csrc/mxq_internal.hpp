@@ -27,6 +27,10 @@ hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_
                        int64_t N, int64_t K, int gs, int bits, bool pairs, void* out,
                        hipStream_t s);
 
+// tiled layout -> MLX layout, the inverse of launch_tile (same `pairs` meaning).
+hipError_t launch_untile(const void* tiled, int64_t N, int64_t K, int gs, int bits, bool pairs,
+                         uint32_t* wq, uint16_t* scales, uint16_t* biases, hipStream_t s);
+
 // y[M,N] = x[M,K] * W^T (+ bias): small-M split-K GEMV (any M; rows of x are
 // processed in blocks of up to 8).
 hipError_t launch_qmv(const uint16_t* x, int M, int K, const uint32_t* wq,

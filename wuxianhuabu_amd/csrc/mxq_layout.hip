@@ -317,6 +317,97 @@ __global__ __launch_bounds__(kThreads) void tile_rows_kernel(const uint32_t* __r
   }
 }
 
+// The inverse of tile_rows_kernel, for callers that keep only the tiled copy and
+// need the MLX triple back: one workgroup per (row block, group of kTileSteps K
+// steps) reads the records unit by unit (each plane a contiguous 1 KiB per wave),
+// stages the block's rows in LDS, and writes them row by row with consecutive
+// lanes on consecutive 16-byte chunks. The (scale, bias) pair of each group comes
+// from the unit that starts the group. Rows past N (or past N/2 in a half, with
+// `pairs`) are skipped.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void untile_rows_kernel(const uint8_t* __restrict__ in,
+                                                               int64_t N, int64_t K, int gs,
+                                                               bool pairs,
+                                                               uint32_t* __restrict__ wq,
+                                                               uint16_t* __restrict__ scales,
+                                                               uint16_t* __restrict__ biases) {
+  constexpr int CPR = kTileSteps * BITS / 2;
+  constexpr int RSTR = CPR * 16 + 16;
+  __shared__ __attribute__((aligned(16))) uint8_t st[64 * RSTR];
+  const int64_t nk = K / 64;
+  const int64_t ngrp = (nk + kTileSteps - 1) / kTileSteps;
+  const int64_t rb = blockIdx.x / ngrp;
+  const int64_t k0 = (blockIdx.x - rb * ngrp) * kTileSteps;
+  const int64_t rowb = K / 8 * BITS;
+  const int64_t W = K / 32 * BITS;
+  auto dst_row = [&](int t, bool& valid) {
+    const int h = t >> 5, r = t & 31;
+    const int64_t row = pairs ? h * (N / 2) + rb * 32 + r : rb * 64 + t;
+    valid = pairs ? rb * 32 + r < N / 2 : row < N;
+    return row;
+  };
+  constexpr int FP = tiled::full_planes(BITS), RW = tiled::rem_words(BITS);
+  const int G = tiled::gps(gs);
+  for (int e = threadIdx.x; e < 128 * kTileSteps; e += kThreads) {
+    const int u = e & 63, h = (e >> 6) & 1, ks = e >> 7;
+    const int64_t kk = k0 + ks;
+    if (kk >= nk) continue;
+    const int r = u & 31, g = u >> 5, t = h * 32 + r;
+    const uint8_t* rec = in + (rb * nk + kk) * tiled::record_bytes(BITS, gs);
+    const uint8_t* half = rec + h * tiled::half_bytes(BITS);
+    uint32_t words[BITS];
+#pragma unroll
+    for (int p = 0; p < FP; ++p) {
+      const u32x4a v = *reinterpret_cast<const u32x4a*>(half + p * 1024 + u * 16);
+      words[4 * p] = v.x; words[4 * p + 1] = v.y; words[4 * p + 2] = v.z; words[4 * p + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+      words[4 * FP + i] = reinterpret_cast<const uint32_t*>(half + FP * 1024 + u * 4 * RW)[i];
+    uint32_t* sw = reinterpret_cast<uint32_t*>(st + t * RSTR + (2 * ks + g) * BITS * 4);
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) sw[i] = words[i];
+    const int64_t c0 = kk * 64 + 32 * g;  // first code of the unit
+    bool valid;
+    const int64_t row = dst_row(t, valid);
+    if (valid && c0 % gs == 0) {
+      const uint32_t sb = reinterpret_cast<const uint32_t*>(rec + tiled::code_bytes(BITS))
+          [(h * 32 + r) * G + (G == 2 ? g : 0)];
+      const int64_t si = row * (K / gs) + c0 / gs;
+      scales[si] = static_cast<uint16_t>(sb & 0xFFFFu);
+      biases[si] = static_cast<uint16_t>(sb >> 16);
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < 64 * CPR; c += kThreads) {
+    const int t = c / CPR, j = c % CPR;
+    bool valid;
+    const int64_t row = dst_row(t, valid);
+    const int64_t off = k0 * 8 * BITS + j * 16;
+    if (!valid || off >= rowb) continue;
+    uint32_t* p = wq + row * W + off / 4;
+    const u32x4a v = *reinterpret_cast<const u32x4a*>(st + t * RSTR + j * 16);
+    if (off + 16 <= rowb) {
+      *reinterpret_cast<u32x4*>(p) = u32x4{v.x, v.y, v.z, v.w};
+    } else {  // the row ends 8 bytes into this chunk
+      *reinterpret_cast<u32x2*>(p) = u32x2{v.x, v.y};
+    }
+  }
+}
+
+template <int BITS>
+struct UntileRun {
+  static hipError_t run(const void* in, int64_t N, int64_t K, int gs, bool pairs, uint32_t* wq,
+                        uint16_t* sc, uint16_t* bi, hipStream_t s) {
+    const int64_t blocks = tiled::row_blocks(N) * ((K / 64 + kTileSteps - 1) / kTileSteps);
+    if (blocks == 0) return hipSuccess;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    untile_rows_kernel<BITS><<<static_cast<unsigned>(blocks), kThreads, 0, s>>>(
+        static_cast<const uint8_t*>(in), N, K, gs, pairs, wq, sc, bi);
+    return hipGetLastError();
+  }
+};
+
 template <int BITS>
 struct TileRun {
   static hipError_t run(const uint32_t* wq, const uint16_t* sc, const uint16_t* bi, int64_t N,
@@ -446,6 +537,11 @@ hipError_t launch_tile(const uint32_t* wq, const uint16_t* scales, const uint16_
                        int64_t N, int64_t K, int gs, int bits, bool pairs, void* out,
                        hipStream_t s) {
   return by_bits<TileRun>(bits, wq, scales, biases, N, K, gs, pairs, out, s);
+}
+
+hipError_t launch_untile(const void* tiled, int64_t N, int64_t K, int gs, int bits, bool pairs,
+                         uint32_t* wq, uint16_t* scales, uint16_t* biases, hipStream_t s) {
+  return by_bits<UntileRun>(bits, tiled, N, K, gs, pairs, wq, scales, biases, s);
 }
 
 hipError_t launch_dequantize(const uint32_t* wq, const void* scales, const void* biases,

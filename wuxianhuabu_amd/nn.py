@@ -15,11 +15,16 @@ to the compute dtype; forward() casts x to bf16, runs the quantized matmul,
 then adds the bias. Here the bias add is fused into the kernel epilogue (added
 in fp32 before the single bf16 rounding).
 
-Both keep the MLX triple as their parameters and, when the geometry allows
-(K % 64 == 0, bf16 scales/biases), also a tiled copy of the same bits built on
-first use; calls then run the tiled kernels, whose results are bit-identical
-to the MLX-layout kernels. The copy costs one more weight's worth of HBM
-(K*N*bits/8 + scale/bias bytes); `tiled=False` turns it off.
+Both hold ONE resident copy of the weight. It starts as the MLX triple; when the
+geometry allows (K % 64 == 0, bf16 scales/biases) the first call tiles it
+(mxq_tile, the same bits reordered) and the triple is dropped, so a layer costs
+K*N*bits/8 bytes of codes plus 4*N*K/gs bytes of scales and biases either way.
+Calls then run the tiled kernels, whose results are bit-identical to the
+MLX-layout kernels. The parameters keep their MLX meaning: reading weight /
+scales / biases (MfLinear: w / scales / biases) returns the triple, rebuilt from
+the tiled copy by mxq_untile (a temporary the caller owns); assigning one of
+them, or update(), replaces the triple and drops the tiled copy, which the next
+call rebuilds. `tiled=False` keeps the triple and runs the MLX-layout kernels.
 """
 import math
 
@@ -29,9 +34,56 @@ from . import ops
 from .weights import get_quantized, infer_geometry
 
 
-class QuantizedLinear:
-    tiled = True  # class default; from_weights / __init__ may override per instance
+class _OneCopy:
+    """The resident copy of a quantized weight: `_triple` (MLX layout) or `_tw` (tiled),
+    never both once tiled (H3MlpW may hand a holder its fc1 pairs-tiled copy)."""
+
+    _triple = None
     _tw = None
+
+    def _parts(self):
+        if self._triple is not None:
+            return self._triple
+        if self._tw is not None:
+            return ops.untile(self._tw)
+        return (None, None, None)
+
+    def _set_part(self, i, value):
+        parts = list(self._parts())
+        parts[i] = value
+        self._triple = tuple(parts)
+        self._tw = None
+
+    def _adopt(self, tw):
+        """Hold `tw` (built from this holder's triple) in place of the triple."""
+        self._tw = tw
+        self._triple = None
+
+    def _plain_tiled(self, K, group_size, bits, enabled):
+        """The plain tiled copy, built from the triple (and replacing it) on first use;
+        None when tiling is off or the geometry does not allow it."""
+        if self._tw is not None:  # a pairs-tiled copy serves only H3MlpW's fused call
+            return None if self._tw.swiglu else self._tw
+        if not enabled or self._triple is None:
+            return None
+        w, s, b = self._parts()
+        if not ops.tiled_supported(K, group_size, bits, s.dtype):
+            return None
+        self._adopt(ops.tile(w, s, b, group_size, bits))
+        return self._tw
+
+
+def _part(i, doc):
+    return property(lambda self: self._parts()[i], lambda self, v: self._set_part(i, v),
+                    doc=doc)
+
+
+class QuantizedLinear(_OneCopy):
+    tiled = True  # class default; from_weights / __init__ may override per instance
+
+    weight = _part(0, "packed codes, uint32 [out, in*bits/32] (MLX layout)")
+    scales = _part(1, "per-group scales [out, in/group_size]")
+    biases = _part(2, "per-group biases [out, in/group_size]")
 
     def __init__(self, input_dims, output_dims, bias=True, group_size=64, bits=4,
                  device="cuda", seed=None, tiled=True):
@@ -47,7 +99,7 @@ class QuantizedLinear:
         scale = math.sqrt(1.0 / self.input_dims)
         w = (torch.rand(self.output_dims, self.input_dims, generator=g) * 2 - 1) * scale
         w = w.to(device=device, dtype=torch.bfloat16)
-        self.weight, self.scales, self.biases = ops.quantized(w, self.group_size, self.bits)
+        self._triple = ops.quantized(w, self.group_size, self.bits)
         self.bias = (torch.zeros(self.output_dims, dtype=torch.bfloat16, device=device)
                      if bias else None)
 
@@ -57,9 +109,8 @@ class QuantizedLinear:
         """Wrap an existing packed triple (as update(parameters:) does)."""
         obj = cls.__new__(cls)
         obj.tiled = bool(tiled)
-        obj.weight = weight
-        obj.scales = scales
-        obj.biases = biases
+        obj._triple = (weight, scales, biases)
+        obj._tw = None
         obj.bias = bias
         obj.group_size = int(group_size)
         obj.bits = int(bits)
@@ -78,14 +129,12 @@ class QuantizedLinear:
         for key in ("weight", "scales", "biases"):
             if key not in parameters:
                 raise KeyError(f"QuantizedLinear.update: missing '{key}'")
-        self.weight = parameters["weight"]
-        self.scales = parameters["scales"]
-        self.biases = parameters["biases"]
+        self._triple = (parameters["weight"], parameters["scales"], parameters["biases"])
+        self._tw = None
         if "bias" in parameters:
             self.bias = parameters["bias"]
-        self.output_dims = int(self.weight.shape[0])
-        self.input_dims = int(self.weight.shape[1] * 32 // self.bits)
-        self._tw = None
+        self.output_dims = int(self._triple[0].shape[0])
+        self.input_dims = int(self._triple[0].shape[1] * 32 // self.bits)
         return self
 
     @property
@@ -93,64 +142,85 @@ class QuantizedLinear:
         return (self.output_dims, self.input_dims)
 
     def tiled_weight(self):
-        """The tiled copy of the weight, built on first use; None when the
-        geometry does not allow one or tiling is off."""
-        if self._tw is None and self.tiled and ops.tiled_supported(
-                self.input_dims, self.group_size, self.bits, self.scales.dtype):
-            self._tw = ops.tile(self.weight, self.scales, self.biases, self.group_size,
-                                self.bits)
-        return self._tw
+        """The tiled copy of the weight, built on first use (it then replaces the
+        triple); None when the geometry does not allow one or tiling is off."""
+        return self._plain_tiled(self.input_dims, self.group_size, self.bits, self.tiled)
 
     def __call__(self, x):
         tw = self.tiled_weight()
         if tw is not None and x.dtype == torch.bfloat16 and x.shape[-1] == tw.K:
             return ops.tiled_matmul(x, tw, bias=self.bias)
-        return ops.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
-                                    group_size=self.group_size, bits=self.bits, bias=self.bias)
+        w, s, b = self._parts()  # argument errors come from the MLX-layout operator
+        return ops.quantized_matmul(x, w, s, b, transpose=True, group_size=self.group_size,
+                                    bits=self.bits, bias=self.bias)
 
     callAsFunction = __call__
 
 
-class MfLinear:
+class _Uncached:
+    """A weights mapping read without its cache, so that a loaded layer holds the only
+    reference to its tensors (SafetensorsFile.get keeps what it reads)."""
+
+    def __init__(self, weights):
+        self._w = weights
+
+    def get(self, key):
+        return self._w.get_uncached(key)
+
+
+class MfLinear(_OneCopy):
     """Dense-or-affine-quantized linear, loaded from a weights mapping."""
+
+    scales = _part(1, "per-group scales [out, in/group_size] (quantized layers)")
+    biases = _part(2, "per-group biases [out, in/group_size] (quantized layers)")
 
     def __init__(self, in_dim, out_dim=0):
         self.in_dim = int(in_dim)
         self.out_dim = int(out_dim)
         self.is_quantized = False
-        self.w = None
-        self.scales = None
-        self.biases = None
+        self._dense = None
         self.bias = None
         self.bits = 0
         self.group_size = 0
         self.tiled = True
-        self._tw = None
         self.lora = None  # LoraAdapters (set_lora), the reference's LoraSlot
+
+    @property
+    def w(self):
+        """packed codes uint32 [out, in*bits/32] (quantized) or the dense weight,
+        pre-transposed [in, out]"""
+        return self._parts()[0] if self.is_quantized else self._dense
+
+    @w.setter
+    def w(self, value):
+        if self.is_quantized:
+            self._set_part(0, value)
+        else:
+            self._dense = value
 
     @classmethod
     def load(cls, weights, prefix, in_features, dtype=torch.bfloat16):
-        """`H3Common.swift:312-338`: quantized triple if present, else dense [out, in]."""
+        """`H3Common.swift:312-338`: quantized triple if present, else dense [out, in].
+        A mapping with get_uncached (SafetensorsFile) is read without its cache."""
         lin = cls(in_features)
-        q = get_quantized(weights, prefix)
+        src = _Uncached(weights) if hasattr(weights, "get_uncached") else weights
+        q = get_quantized(src, prefix)
         if q is not None:
             w, s, b = q
             if w.ndim != 2:
                 raise ValueError(f"bad file: quantized weight rank {w.ndim}")
             lin.out_dim = int(w.shape[0])
             lin.is_quantized = True
-            lin.w = w
             lin.bits, lin.group_size = infer_geometry(int(w.shape[1]), int(s.shape[1]),
                                                       in_features)
-            lin.scales = s.to(dtype).contiguous()
-            lin.biases = b.to(dtype).contiguous()
+            lin._triple = (w, s.to(dtype).contiguous(), b.to(dtype).contiguous())
         else:
-            raw = weights.get(prefix + ".weight")
+            raw = src.get(prefix + ".weight")
             if raw is None:
                 raise KeyError(f"missing weight: {prefix}.weight")
             lin.out_dim = int(raw.shape[0])
-            lin.w = raw.t().to(dtype).contiguous()  # dense, pre-transposed [in, out]
-        b = weights.get(prefix + ".bias")
+            lin._dense = raw.t().to(dtype).contiguous()  # dense, pre-transposed [in, out]
+        b = src.get(prefix + ".bias")
         if b is not None:
             lin.bias = b.to(dtype).contiguous()
         return lin
@@ -163,29 +233,31 @@ class MfLinear:
         return self
 
     def tiled_weight(self):
-        if self._tw is None and self.is_quantized and self.tiled and ops.tiled_supported(
-                self.in_dim, self.group_size, self.bits, self.scales.dtype):
-            self._tw = ops.tile(self.w, self.scales, self.biases, self.group_size, self.bits)
-        return self._tw
+        """The plain tiled copy, built on first use (it then replaces the triple)."""
+        if not self.is_quantized:
+            return None
+        return self._plain_tiled(self.in_dim, self.group_size, self.bits, self.tiled)
 
     def forward(self, x):
         """`H3Common.swift:341-377`: bf16 quantized matmul, + bias, + the LoRA term. On
         tiled weights the LoRA term joins the fp32 accumulators in the kernel, before
         the bias and the one rounding."""
         if self.is_quantized:
-            if self.scales.dtype != torch.bfloat16:
-                raise ValueError("MfLinear: the quantized kernels take bfloat16 scales/biases")
             xc = x.to(torch.bfloat16).contiguous()
             tw = self.tiled_weight()
             if tw is not None:
                 return ops.tiled_matmul(xc, tw, bias=self.bias, lora=self.lora)
-            out = ops.quantized_matmul(xc, self.w, self.scales, self.biases, transpose=True,
-                                       group_size=self.group_size, bits=self.bits,
-                                       bias=self.bias)
+            # the MLX-layout kernels: untiled weights, or fc1 while H3MlpW holds it tiled in
+            # gate/up pairs (rebuilt as a temporary triple)
+            w, s, b = self._parts()
+            if s.dtype != torch.bfloat16:
+                raise ValueError("MfLinear: the quantized kernels take bfloat16 scales/biases")
+            out = ops.quantized_matmul(xc, w, s, b, transpose=True, group_size=self.group_size,
+                                       bits=self.bits, bias=self.bias)
         else:
             # dense branch: not part of the quantized path; plain device matmul
-            xc = x.to(self.w.dtype)
-            out = xc @ self.w
+            xc = x.to(self._dense.dtype)
+            out = xc @ self._dense
             if self.bias is not None:
                 out = out + self.bias
         if self.lora is not None:
@@ -233,7 +305,6 @@ class H3MlpW:
 
     def __init__(self, fc1, fc2):
         self.fc1, self.fc2 = fc1, fc2
-        self._tw_pairs = None
 
     @classmethod
     def load(cls, weights, prefix, hidden_size, ffn_hidden, dtype=torch.bfloat16):
@@ -242,12 +313,17 @@ class H3MlpW:
                    MfLinear.load(weights, prefix + ".fc2", ffn_hidden, dtype))
 
     def _pairs(self):
+        """fc1 tiled in gate/up pairs; fc1 then holds this copy in place of its own."""
         f = self.fc1
-        if (self._tw_pairs is None and f.is_quantized and f.tiled and f.out_dim % 2 == 0 and
-                ops.tiled_supported(f.in_dim, f.group_size, f.bits, f.scales.dtype)):
-            self._tw_pairs = ops.tile(f.w, f.scales, f.biases, f.group_size, f.bits,
-                                      swiglu=True)
-        return self._tw_pairs
+        if f._tw is not None and f._tw.swiglu:
+            return f._tw
+        if not (f.is_quantized and f.tiled and f.out_dim % 2 == 0):
+            return None
+        w, s, b = f._parts()
+        if not ops.tiled_supported(f.in_dim, f.group_size, f.bits, s.dtype):
+            return None
+        f._adopt(ops.tile(w, s, b, f.group_size, f.bits, swiglu=True))
+        return f._tw
 
     def forward(self, x):
         tw = self._pairs()

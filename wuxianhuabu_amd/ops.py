@@ -261,6 +261,23 @@ def tile(w, scales, biases, group_size=64, bits=4, *, swiglu=False):
     return TiledWeight(data, N, K, group_size, bits, swiglu)
 
 
+def untile(tw):
+    """TiledWeight -> the MLX-layout triple (wq uint32 [N, K*bits/32], bf16 scales and
+    biases [N, K/group_size]) holding the same bits as the triple it was tiled from
+    (swiglu weights come back with their [gate; up] row order)."""
+    if not isinstance(tw, TiledWeight):
+        raise ValueError(f"[untile] expected a TiledWeight (got {type(tw).__name__}).")
+    dev = tw.device
+    wq = torch.empty((tw.N, tw.K * tw.bits // 32), dtype=torch.uint32, device=dev)
+    scales = torch.empty((tw.N, tw.K // tw.group_size), dtype=torch.bfloat16, device=dev)
+    biases = torch.empty_like(scales)
+    L = _lib.lib()
+    fn = L.mxq_untile_swiglu if tw.swiglu else L.mxq_untile
+    _lib.check(fn(_ptr(tw.data), tw.N, tw.K, tw.group_size, tw.bits, _ptr(wq), _ptr(scales),
+                  _ptr(biases), _stream(tw.data)))
+    return wq, scales, biases
+
+
 _ACTIVATIONS = {None: _lib.MXQ_ACT_NONE, "gelu_tanh": _lib.MXQ_ACT_GELU_TANH,
                 "swiglu": _lib.MXQ_ACT_SWIGLU}
 
