@@ -20,6 +20,8 @@ from .ops import (LoraAdapters, TiledWeight, dequantized, pack, quantized,  # no
                   quantizedMatmul, quantizedMM, tile, tiled_matmul, tiled_supported, unpack,
                   untile)
 from .weights import get_quantized, header_candidates, infer_geometry  # noqa: F401
+from .convert import (QuantizedLinearModule, quantize_checkpoint, quantize_module,  # noqa: F401
+                      should_quant)
 
 __all__ = [
     "quantized", "dequantized", "quantized_matmul", "quantizedMatmul", "quantizedMM",
@@ -28,5 +30,6 @@ __all__ = [
     "QuantizedLinear", "MfLinear", "LTXFFN", "H3MlpW", "SafetensorsFile", "get_quantized",
     "infer_geometry", "header_candidates", "lib", "LIB_PATH", "MXQError",
     "fused_norm_modscale", "fused_norm_modscale_row", "fused_mod_gate", "fused_rmsnorm_rope",
-    "build_row_mod_map",
+    "build_row_mod_map", "quantize_checkpoint", "quantize_module", "QuantizedLinearModule",
+    "should_quant",
 ]

@@ -102,6 +102,15 @@ class SafetensorsFile:
                                           ctypes.c_void_p(out.data_ptr())))
         return out
 
+    def read_bytes(self, key):
+        """The tensor's bytes as a host uint8 array, whatever its dtype."""
+        _, _, nbytes = self.info(key)
+        out = np.empty(nbytes, dtype=np.uint8)
+        if nbytes:
+            _lib.check(_lib.lib().mxq_st_read_host(self._handle(), key.encode(),
+                                                   out.ctypes.data_as(ctypes.c_void_p)))
+        return out
+
     def get_quantized(self, prefix):
         """(weight, scales, biases) for `prefix` in either key spelling, or None."""
         return get_quantized(self, prefix)
@@ -118,7 +127,7 @@ class SafetensorsFile:
             if not k.endswith(".weight"):
                 continue
             dt, shape, _ = self.info(k)
-            if dt != "U32" or len(shape) != 2:
+            if dt != "U32" or len(shape) != 2 or shape[0] == 0:  # no rows: nothing to score
                 continue
             base = k[: -len("weight")]
             for sk, bk in ((base + "scales", base + "biases"),
