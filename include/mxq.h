@@ -35,7 +35,7 @@
  *   - All tensor pointers are DEVICE pointers, row-major and contiguous,
  *     owned by the caller. Functions enqueue on `stream` (a hipStream_t;
  *     NULL = the default stream) and return without synchronising.
- *   - No function allocates device memory.
+ *   - No function allocates device memory, except mxq_malloc (below).
  *   - Packed layout: for output row n, code k occupies bits [k*bits, k*bits+bits)
  *     of the little-endian bitstream formed by wq[n, 0..K*bits/32).
  *     scales, biases: [rows, K/group_size]; w = q*scale + bias.
@@ -310,6 +310,20 @@ const char* mxq_status_string(int status);
 /* Blocks until all work on `stream` has finished; reports asynchronous kernel
  * errors as MXQ_ERR_HIP. */
 int mxq_stream_synchronize(mxq_stream stream);
+
+/* ---- device memory and streams, for hosts that do not link HIP themselves ----
+ * (the Swift bridge, C programs). The reference's rule for buffers holds here:
+ * free device memory only after the work that uses it has finished, i.e. after
+ * synchronizing the stream it was used on (`model/minimax h3/H3Pipeline.swift:
+ * 212-228`, Stream.gpu.synchronize() before buffers are released). */
+int mxq_stream_create(mxq_stream* stream); /* a new stream of default priority */
+int mxq_stream_destroy(mxq_stream stream); /* NULL: no-op */
+int mxq_malloc(void** ptr, size_t bytes);  /* device memory; bytes == 0 gives NULL */
+int mxq_free(void* ptr);                   /* NULL: no-op */
+/* Copies between host and device memory on `stream`; both return once the copy
+ * (and all earlier work on the stream) has finished, so `src` may then be reused. */
+int mxq_copy_to_device(void* dst, const void* src, size_t bytes, mxq_stream stream);
+int mxq_copy_to_host(void* dst, const void* src, size_t bytes, mxq_stream stream);
 
 /* MXQ_ABI_VERSION of the loaded library. */
 int mxq_abi_version(void);

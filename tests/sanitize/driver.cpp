@@ -182,6 +182,19 @@ int api(uint64_t seed, int count) {
     mxq_norm_modscale(x, M, K, w, s, c, N, static_cast<const uint32_t*>(t), 1e-6f, y, nullptr);
     mxq_mod_gate(x, w, M, K, s, N, static_cast<const uint32_t*>(t), y, nullptr);
     mxq_rmsnorm_rope(x, M, N, K, w, s, c, dt, static_cast<int>(R & 1023), 1e-6f, y, nullptr);
+    {  // the memory and stream helpers ("device" memory is host memory in this build)
+      mxq_stream st = nullptr;
+      void* d = nullptr;
+      unsigned char h[32] = {0};
+      const size_t n = static_cast<size_t>(below(3)) * 16;
+      mxq_stream_create(below(8) ? &st : nullptr);
+      mxq_malloc(below(8) ? &d : nullptr, n);
+      mxq_copy_to_device(below(6) ? d : nullptr, h, n, st);
+      mxq_copy_to_host(h, below(6) ? d : nullptr, n, st);
+      mxq_stream_synchronize(st);
+      mxq_free(d);
+      mxq_stream_destroy(st);
+    }
     mxq_status_string(static_cast<int>(below(12)) - 8);
     (void)mxq_last_error();
   }

@@ -20,7 +20,8 @@ enum : int { hipSuccess = 0, hipErrorInvalidValue = 1, hipErrorOutOfMemory = 2,
              hipErrorNotSupported = 801 };
 typedef struct ihipStream_t* hipStream_t;
 typedef struct ihipEvent_t* hipEvent_t;
-enum hipMemcpyKind { hipMemcpyHostToHost = 0, hipMemcpyHostToDevice = 1 };
+enum hipMemcpyKind { hipMemcpyHostToHost = 0, hipMemcpyHostToDevice = 1,
+                     hipMemcpyDeviceToHost = 2 };
 #define hipHostMallocDefault 0u
 #define hipEventDisableTiming 2u
 
@@ -39,6 +40,22 @@ inline hipError_t hipMemcpyAsync(void* dst, const void* src, size_t n, hipMemcpy
   return hipSuccess;
 }
 inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+inline hipError_t hipStreamCreate(hipStream_t* s) {
+  *s = reinterpret_cast<hipStream_t>(std::malloc(1));
+  return *s ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipStreamDestroy(hipStream_t s) {
+  std::free(s);
+  return hipSuccess;
+}
+inline hipError_t hipMalloc(void** p, size_t n) {
+  *p = std::malloc(n);
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipFree(void* p) {
+  std::free(p);
+  return hipSuccess;
+}
 inline hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) {
   *e = reinterpret_cast<hipEvent_t>(std::malloc(1));
   return *e ? hipSuccess : hipErrorOutOfMemory;

@@ -157,7 +157,7 @@ def test_mflinear_and_h3mlp_hold_one_copy(dev, O, tmp_path):
     for name, n, k in (("mlp.fc1", 2 * F, H), ("mlp.fc2", H, F)):
         _, wq, s, b, _ = make_case(O, 1, n, k, gs, bits, seed=n + k)
         parts[name] = (wq, s, b)
-        tensors[name + ".weight"] = torch.from_numpy(wq.view(np.int32))
+        tensors[name + ".weight"] = torch.from_numpy(wq.view(np.int32)).view(torch.uint32)
         tensors[name + ".scales"] = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
         tensors[name + ".biases"] = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
     path = tmp_path / "mlp.safetensors"

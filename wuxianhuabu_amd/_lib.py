@@ -48,6 +48,12 @@ SIGNATURES = {
     "mxq_tile_swiglu": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp]),
     "mxq_untile": (_int, [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp]),
     "mxq_untile_swiglu": (_int, [_vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp]),
+    "mxq_stream_create": (_int, [_vp]),
+    "mxq_stream_destroy": (_int, [_vp]),
+    "mxq_malloc": (_int, [_vp, ctypes.c_size_t]),
+    "mxq_free": (_int, [_vp]),
+    "mxq_copy_to_device": (_int, [_vp, _vp, ctypes.c_size_t, _vp]),
+    "mxq_copy_to_host": (_int, [_vp, _vp, ctypes.c_size_t, _vp]),
     "mxq_norm_modscale": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, ctypes.c_float,
                                  _vp, _vp]),
     "mxq_mod_gate": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),

@@ -146,6 +146,53 @@ int mxq_stream_synchronize(mxq_stream stream) {
   return hip_status("synchronize", hipStreamSynchronize(static_cast<hipStream_t>(stream)));
 }
 
+int mxq_stream_create(mxq_stream* stream) {
+  if (!stream) return fail(MXQ_ERR_NULL, "[stream_create] stream must be non-NULL.");
+  hipStream_t s = nullptr;
+  const int rc = hip_status("stream_create", hipStreamCreate(&s));  // default priority
+  *stream = rc == MXQ_OK ? static_cast<mxq_stream>(s) : nullptr;
+  return rc;
+}
+
+int mxq_stream_destroy(mxq_stream stream) {
+  if (!stream) return ok();
+  return hip_status("stream_destroy", hipStreamDestroy(static_cast<hipStream_t>(stream)));
+}
+
+int mxq_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(MXQ_ERR_NULL, "[malloc] ptr must be non-NULL.");
+  *ptr = nullptr;
+  if (bytes == 0) return ok();
+  const int rc = hip_status("malloc", hipMalloc(ptr, bytes));
+  if (rc != MXQ_OK) *ptr = nullptr;
+  return rc;
+}
+
+int mxq_free(void* ptr) {
+  if (!ptr) return ok();
+  return hip_status("free", hipFree(ptr));
+}
+
+namespace {
+int copy_sync(const char* op, void* dst, const void* src, size_t bytes, hipMemcpyKind kind,
+              mxq_stream stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(MXQ_ERR_NULL, "[%s] dst and src must be non-NULL.", op);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return hip_status(op, e);
+}
+}  // namespace
+
+int mxq_copy_to_device(void* dst, const void* src, size_t bytes, mxq_stream stream) {
+  return copy_sync("copy_to_device", dst, src, bytes, hipMemcpyHostToDevice, stream);
+}
+
+int mxq_copy_to_host(void* dst, const void* src, size_t bytes, mxq_stream stream) {
+  return copy_sync("copy_to_host", dst, src, bytes, hipMemcpyDeviceToHost, stream);
+}
+
 int mxq_pack(const uint8_t* codes, int64_t rows, int64_t cols, int bits, uint32_t* wq,
              mxq_stream stream) {
   if (!bits_supported(bits))
