@@ -256,6 +256,13 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 //   sum_k x_k (s q_k + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k.
 // 8-bit codes (up to 255) are converted exactly instead, with offset 0.
 // ---------------------------------------------------------------------------
+// Cache policy of the tiled weight loads: non-temporal, since each weight byte is read
+// once (M = 2, K = 4096, N = 24576, 6-bit: 16.3 against 17.5 us; the Gemma logits
+// shape 95.9 against 106.3 us). The MLX-layout form keeps the default: its batches
+// split a row's 128-byte lines, and the next batch reads the rest of a line from L2
+// (25.6 us; 38.1 with non-temporal loads). The activations, which every workgroup
+// reads, keep the default too.
+constexpr int kTiledWeightAux = 2;
 typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
@@ -310,6 +317,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // some MFMA results over their own A or B operand registers, which gave
   // timing-dependent wrong sums.
   asm volatile("" ::: "a0");
+  constexpr int kWeightAux = MLX ? 0 : kTiledWeightAux;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g2 = lane >> 5;
@@ -445,7 +453,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
         for (int nb = 0; nb < NH; ++nb)
           B.wc[nb][i] = __builtin_amdgcn_raw_buffer_load_b128(
               wrs, min((h0 + nb) * 32 + (tc & 0xFF), rows - 1) * rowb + sb0 + (tc >> 8) * 16, 0,
-              0);
+              kWeightAux);
       }
     }
 #pragma unroll
@@ -458,17 +466,18 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
         if constexpr (!MLX) {
 #pragma unroll
           for (int p = 0; p < FP; ++p) {
-            const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, 0);
+            const v4u_t v =
+                __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo[nb] + p * 1024, so, kWeightAux);
             B.w[j][nb][4 * p] = v.x; B.w[j][nb][4 * p + 1] = v.y;
             B.w[j][nb][4 * p + 2] = v.z; B.w[j][nb][4 * p + 3] = v.w;
           }
           if constexpr (RW == 1) {
-            B.w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, 0);
+            B.w[j][nb][4 * FP] = __builtin_amdgcn_raw_buffer_load_b32(wrs, rvo[nb], so, kWeightAux);
           } else if constexpr (RW == 2) {
-            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, 0);
+            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, rvo[nb], so, kWeightAux);
             B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
           } else if constexpr (RW == 3) {
-            const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, 0);
+            const v3u_t v = __builtin_amdgcn_raw_buffer_load_b96(wrs, rvo[nb], so, kWeightAux);
             B.w[j][nb][4 * FP] = v.x; B.w[j][nb][4 * FP + 1] = v.y;
             B.w[j][nb][4 * FP + 2] = v.z;
           }
@@ -476,19 +485,19 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
         if constexpr (MLX) {
           if constexpr (GP == 2) {  // groups 2k and 2k + 1
             const int ss = __builtin_amdgcn_readfirstlane(kj * 4);
-            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], ss, 0);
-            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo[nb], ss, 0);
+            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], ss, kWeightAux);
+            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo[nb], ss, kWeightAux);
           } else {                  // group k >> gshift
             const int ss = __builtin_amdgcn_readfirstlane((kj >> gshift) * 2);
-            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, 0);
-            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, 0);
+            B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b16(srs, svo[nb], ss, kWeightAux);
+            B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b16(brs, svo[nb], ss, kWeightAux);
           }
         } else if constexpr (GP == 2) {
-          const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, svo[nb], so, 0);
+          const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(wrs, svo[nb], so, kWeightAux);
           B.sb[j][nb][0] = v.x;
           B.sb[j][nb][GP - 1] = v.y;
         } else {
-          B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, 0);
+          B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, kWeightAux);
         }
       }
     }
@@ -656,11 +665,20 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   }
 }
 
-// Launch shape (measured at M = 1, 2 and 8 for K = 4096, N = 24576 among 2-8
-// waves x 1-8 steps per batch, with the two register sets): one workgroup per
-// 32-row record half (768 workgroups at N = 24576, three per CU), 4 waves,
-// batches of 2 steps.
-constexpr int kTiledNH = 1, kTiledWaves = 4, kTiledSPW = 2;
+// Launch shape: one workgroup per 32-row record half (768 workgroups at N = 24576,
+// three per CU), 4 waves, batches of 1 step (two steps in flight per wave). Measured
+// with non-temporal weight loads in a same-box A/B at K = 4096, N = 24576, 6-bit, five
+// rotated copies (median of 7 x 50 launches): 1-step batches 14.4 us at M = 2 (14.4 at
+// M = 1, 15.4 at M = 8); 2-step 14.9 (14.6, 17.8); 3-step 16.1; 4-step 15.7; 8 waves
+// with 2-step batches 15.1 (21.4 at M = 8), with 1-step 15.2. Results are the same bits
+// for every batch size (each wave sums its K span in step order).
+#ifndef MXQ_QMV_WAVES
+#define MXQ_QMV_WAVES 4
+#endif
+#ifndef MXQ_QMV_SPW
+#define MXQ_QMV_SPW 1
+#endif
+constexpr int kTiledNH = 1, kTiledWaves = MXQ_QMV_WAVES, kTiledSPW = MXQ_QMV_SPW;
 
 template <int BITS, int MT>
 hipError_t run_qmv_tiled(const uint16_t* x, int M, int K, const void* tw, int N, int gs,
@@ -686,7 +704,10 @@ hipError_t run_qmv_mlx(const uint16_t* x, int M, int K, const uint32_t* wq, cons
   // at 6 bits), so fewer of a row's 128-byte lines are split between batches
   // (M = 2, N = 24576: 31.4 us against 32.8 us with 2 steps; 8 or 16 steps, two
   // record halves per workgroup or 2 waves per workgroup were slower)
-  constexpr int NH = 1, WPB = 4, SPW = 4;
+#ifndef MXQ_QMV_MLX_SPW
+#define MXQ_QMV_MLX_SPW 4
+#endif
+  constexpr int NH = 1, WPB = 4, SPW = MXQ_QMV_MLX_SPW;
   dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
   if (gs == 32)
     qmv_tiled_kernel<BITS, MT, 2, NH, WPB, SPW, true><<<grid, 64 * WPB, 0, s>>>(
