@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
   constexpr int WSTAGE = 4 * R::BYTES; // bytes per weight stage
   constexpr int L = XL + R::LOADS;     // requests per wave per step
   constexpr int SLOTS = MB * 4;        // MFMA pairs per step
-  static_assert(L <= SLOTS, "one request per MFMA pair at most");
+  static_assert(L <= 2 * SLOTS, "two requests per MFMA pair at most");
   // epilogue staging: 4 KiB per wave, inside the consumed activation stage when
   // the wave's part of it is that large (BM >= 128), else a separate area
   constexpr bool OWN_STAGING = XL * 1024 < 4096;
@@ -593,11 +593,14 @@ hipError_t run_tiled(const uint16_t* x, int M, int K, const void* tw, int N,
   return hipGetLastError();
 }
 
-// Time of one 64- or 128-token tile relative to a 256-token tile (same K, same
-// 256 features): the weight loads and unpacking do not shrink with the tile.
-constexpr double kTileCost64 = 0.6, kTileCost128 = 0.75;
+// Time of one 32-, 64- or 128-token tile relative to a 256-token tile (same K,
+// same 256 features): the weight loads and unpacking do not shrink with the tile,
+// and a short step is bound by the ring's latency (K = 4096, N = 16384, 6-bit:
+// 48.7 us for 32 tokens in 32-row tiles, 50.4 us for 64 tokens in 32-row tiles and
+// 52.9 us in 64-row tiles, against 1.52 ms for 14 rounds of 256-row tiles).
+constexpr double kTileCost32 = 0.45, kTileCost64 = 0.6, kTileCost128 = 0.75;
 
-// Token tiles of 64, 128 or 256 rows, chosen by estimated time: rounds of
+// Token tiles of 32, 64, 128 or 256 rows, chosen by estimated time: rounds of
 // tiles over the CUs times the relative cost of one tile. Small problems (few
 // 256-row tiles, e.g. M = 256 with N = 2048: 8 tiles for 256 CUs) take the
 // smaller tiles, which spread the same work over more CUs. When M % 256
@@ -607,43 +610,54 @@ constexpr double kTileCost64 = 0.6, kTileCost128 = 0.75;
 // accumulates each output in the same order, so the choice never changes a
 // result bit.
 template <int BITS, int GP>
+hipError_t run_rows(int bm, const uint16_t* x, int M, int K, const void* tw, int N,
+                    const uint16_t* bias, int act, const Lora& lo, uint16_t* y, hipStream_t s) {
+  switch (bm) {
+    case 32: return run_tiled<BITS, 32, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+    case 64: return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+    case 128: return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+    default: return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  }
+}
+
+template <int BITS, int GP>
 hipError_t pick_rows(const uint16_t* x, int M, int K, const void* tw, int N,
                      const uint16_t* bias, int act, const Lora& lo, uint16_t* y,
                      hipStream_t s) {
-  if (M <= 64) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
   const int64_t cus = cu_count(), n_tiles = (N + kRows - 1) / kRows;
   auto rounds = [&](int64_t tiles) { return static_cast<double>((tiles + cus - 1) / cus); };
-  const double t64 = rounds((M + 63) / 64 * n_tiles) * kTileCost64;
-  const double t128 = rounds((M + 127) / 128 * n_tiles) * kTileCost128;
-  if (M <= 128) {
-    if (t64 < t128) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
-    return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
-  }
+  const int heights[4] = {32, 64, 128, 256};
+  const double costs[4] = {kTileCost32, kTileCost64, kTileCost128, 1.0};
+  // one launch of the best height for `rows` tokens: (estimated time, height)
+  auto best = [&](int64_t rows, int max_bm, int& bm_out) {
+    double t_best = 0;
+    bm_out = 0;
+    for (int h = 0; h < 4 && heights[h] <= max_bm; ++h) {
+      const double t = rounds((rows + heights[h] - 1) / heights[h] * n_tiles) * costs[h];
+      if (bm_out == 0 || t < t_best) {
+        t_best = t;
+        bm_out = heights[h];
+      }
+    }
+    return t_best;
+  };
+  int bm = 0;
+  const double t_one = best(M, 256, bm);
   const int full = M / 256, rem = M % 256;
-  const int64_t t_full = static_cast<int64_t>(full) * n_tiles;
-  const double one = rounds((M + 255) / 256 * n_tiles);
-  double t256 = one;
-  bool split = false;
-  if (rem > 0 && rem <= 128) {
-    const double two = rounds(t_full) + rounds(n_tiles) * (rem <= 64 ? kTileCost64 : kTileCost128);
-    if (two < one) {
-      t256 = two;
-      split = true;
+  if (full > 0 && rem > 0 && rem <= 128) {
+    int bm_rem = 0;
+    const double t_two = rounds(static_cast<int64_t>(full) * n_tiles) + best(rem, 128, bm_rem);
+    if (t_two < t_one) {
+      const hipError_t e = run_rows<BITS, GP>(256, x, full * 256, K, tw, N, bias, act, lo, y, s);
+      if (e != hipSuccess) return e;
+      const int64_t r0 = static_cast<int64_t>(full) * 256;
+      const int64_t ldy = act == MXQ_ACT_SWIGLU ? N / 2 : N;
+      const Lora rl{lo.xa ? lo.xa + r0 * lo.R : nullptr, lo.bt, lo.R};
+      return run_rows<BITS, GP>(bm_rem, x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy,
+                                s);
     }
   }
-  if (t64 < t256 && t64 <= t128) return run_tiled<BITS, 64, GP>(x, M, K, tw, N, bias, act, lo, y, s);
-  if (t128 < t256) return run_tiled<BITS, 128, GP>(x, M, K, tw, N, bias, act, lo, y, s);
-  if (split) {
-    const hipError_t e = run_tiled<BITS, 256, GP>(x, full * 256, K, tw, N, bias, act, lo, y, s);
-    if (e != hipSuccess) return e;
-    const int64_t r0 = static_cast<int64_t>(full) * 256;
-    const int64_t ldy = act == MXQ_ACT_SWIGLU ? N / 2 : N;
-    const Lora rl{lo.xa ? lo.xa + r0 * lo.R : nullptr, lo.bt, lo.R};
-    if (rem <= 64)
-      return run_tiled<BITS, 64, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy, s);
-    return run_tiled<BITS, 128, GP>(x + r0 * K, rem, K, tw, N, bias, act, rl, y + r0 * ldy, s);
-  }
-  return run_tiled<BITS, 256, GP>(x, M, K, tw, N, bias, act, lo, y, s);
+  return run_rows<BITS, GP>(bm, x, M, K, tw, N, bias, act, lo, y, s);
 }
 
 template <int BITS>
