@@ -235,6 +235,20 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s, checks=()):
         "sample": f"{nrows} of {qmm_c['M']} rows of the qmm workload (mlx CPU qmm loop "
                   f"restated in C, bf16 arithmetic), {t:.1f} s; the loop is linear in M",
     }
+    # the same loop with an fp32 running sum and fp32 products (the variant BASELINE
+    # times beside the bf16 one), 1 core, a third of the budget
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=1, rows=[0], threads=1)
+    t_row = time.perf_counter() - t0
+    nrows32 = int(max(1, min(256, budget_s / 3 / max(t_row, 1e-3))))
+    t0 = time.perf_counter()
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=1,
+                  rows=np.arange(nrows32, dtype=np.int64), threads=1)
+    t32 = time.perf_counter() - t0
+    out["cpu_baseline_fp32acc"] = {
+        "value": 2.0 * nrows32 * N * K / t32 / 1e12, "unit": "TFLOP/s", "cores": 1,
+        "kind": "port",
+        "sample": f"{nrows32} of {qmm_c['M']} rows, {t32:.1f} s, fp32 products and sum"}
     # the same loop over all host cores this process may use (OpenMP over N), on a
     # sample sized to the same budget
     nthr = threads
