@@ -4,7 +4,8 @@ against mxq_quantized_matmul_ws (a caller workspace), through the C ABI.
 Two calls in a row, the second with a smaller input, give the bits of the workspace
 entry point each time (the array keeps the first call's tiled weight; the second
 call overwrites what it uses). A small M takes the plain operator; a weight whose
-tiled copy exceeds the array is refused before anything is enqueued.
+tiled copy exceeds the array is refused before anything is enqueued. Captured in a HIP
+graph (the callers it is for), every replay gives the same bits.
 """
 import ctypes
 
@@ -101,3 +102,34 @@ def test_noalloc_refuses_a_weight_above_the_scratch(dev):
     assert b"scratch" in L.mxq_last_error()
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())
+
+
+def test_noalloc_under_graph_capture(dev, O):
+    """The calls it is for: captured in a HIP graph (nothing allocated, no memset node),
+    the graph replayed three times with eager work and synchronizations between the
+    replays (an eager call on another weight overwrites the shared array each time);
+    every replay gives the workspace entry point's bits."""
+    L = _lib.lib()
+    M, N, K, gs, bits = 1536, 2048, 2048, 64, 6
+    _, d = _inputs(O, dev, M, N, K, gs, bits, 21)
+    _, d2 = _inputs(O, dev, 1100, 1024, 1024, 32, 4, 22)
+    y_ref = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    rc, _ = _with_workspace(L, d, M, N, K, gs, bits, y_ref)
+    assert rc == _lib.MXQ_OK
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    y2 = torch.empty(1100, 1024, dtype=torch.bfloat16, device=dev)
+    # outside capture first: the library looks up the array's address and the CU count once
+    assert _noalloc(L, d, M, N, K, gs, bits, y) == _lib.MXQ_OK
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = _noalloc(L, d, M, N, K, gs, bits, y)
+    assert rc == _lib.MXQ_OK, L.mxq_last_error()
+    for i in range(3):
+        y.fill_(float("nan"))
+        assert _noalloc(L, d2, 1100, 1024, 1024, 32, 4, y2) == _lib.MXQ_OK
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"replay {i}"
