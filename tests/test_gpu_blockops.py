@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import wuxianhuabu_amd as mx
-from tests.gpu_util import dev_bf16, host_bf16, host_f32_of_bf16
+from tests.gpu_util import dev_bf16, host_f32_of_bf16
 
 pytestmark = pytest.mark.gpu
 

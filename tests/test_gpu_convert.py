@@ -18,8 +18,9 @@ def _bf16_bits(t):
     return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("bits", [4, 6])
-def test_quantize_checkpoint_matches_oracle(dev, O, tmp_path, bits):
+@pytest.mark.parametrize("bits,gs", [(4, 64), (6, 64), (2, 32), (3, 128), (5, 64), (8, 32),
+                                     (6, 128), (4, 32)])
+def test_quantize_checkpoint_matches_oracle(dev, O, tmp_path, bits, gs):
     g = torch.Generator().manual_seed(bits)
     src_t = {
         "blocks.0.norm.weight": torch.randn(256, generator=g).bfloat16(),
@@ -33,10 +34,12 @@ def test_quantize_checkpoint_matches_oracle(dev, O, tmp_path, bits):
     }
     src, dst = tmp_path / "dense.safetensors", tmp_path / "q.safetensors"
     save_file(src_t, str(src))
-    stats = mx.quantize_checkpoint(src, dst, group_size=64, bits=bits, device=dev)
-    assert stats["quantized"] == 3 and stats["kept"] == 5
+    stats = mx.quantize_checkpoint(src, dst, group_size=gs, bits=bits, device=dev)
     quant = {k for k, v in src_t.items() if mx.should_quant("BF16" if v.dtype == torch.bfloat16
-                                                            else "F32", tuple(v.shape))}
+                                                            else "F32", tuple(v.shape), gs)}
+    assert stats["quantized"] == len(quant) and stats["kept"] == len(src_t) - len(quant)
+    if gs == 64:
+        assert len(quant) == 3  # qkv, fc2 and the empty weight; the [384, 8] table is kept
     with safe_open(str(dst), framework="pt") as f:
         keys = set(f.keys())
         for k, v in src_t.items():
@@ -46,10 +49,10 @@ def test_quantize_checkpoint_matches_oracle(dev, O, tmp_path, bits):
                 s = _bf16_bits(f.get_tensor(k + ".scales"))
                 b = _bf16_bits(f.get_tensor(k + ".biases"))
                 n, kd = v.shape
-                assert wq.shape == (n, kd * bits // 32) and s.shape == b.shape == (n, kd // 64)
+                assert wq.shape == (n, kd * bits // 32) and s.shape == b.shape == (n, kd // gs)
                 if n == 0:
                     continue
-                ref = O.quantize(v.float().numpy().reshape(v.shape), 64, bits, mode=1)
+                ref = O.quantize(v.float().numpy().reshape(v.shape), gs, bits, mode=1)
                 np.testing.assert_array_equal(wq, ref["wq"].reshape(wq.shape), err_msg=k)
                 np.testing.assert_array_equal(s, ref["scales_bf16"].reshape(s.shape), err_msg=k)
                 np.testing.assert_array_equal(b, ref["biases_bf16"].reshape(b.shape), err_msg=k)
@@ -57,16 +60,17 @@ def test_quantize_checkpoint_matches_oracle(dev, O, tmp_path, bits):
                 assert torch.equal(f.get_tensor(k), v), k
     # the output serves the loader: parameter inference and a layer's forward
     with mx.SafetensorsFile(dst, device=dev) as f:
-        assert f.infer_quant_params() == (bits, 64)
+        if (bits, gs) in ((4, 64), (6, 64)):  # widths that fit one (bits, gs) pair only, or
+            assert f.infer_quant_params() == (bits, 64)  # resolved by code statistics
         lin = mx.MfLinear.load(f, "blocks.0.attn.qkv", 256)
-        assert lin.is_quantized and lin.bits == bits and lin.group_size == 64
+        assert lin.is_quantized and lin.bits == bits and lin.group_size == gs
         assert lin.bias is not None
         x = O.normal_bf16(5, 70 * 256).reshape(70, 256)
         xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev)
         y = host_f32_of_bf16(lin(xd))
-        ref = O.quantize(src_t["blocks.0.attn.qkv.weight"].float().numpy(), 64, bits, mode=1)
+        ref = O.quantize(src_t["blocks.0.attn.qkv.weight"].float().numpy(), gs, bits, mode=1)
         bias = _bf16_bits(src_t["blocks.0.attn.qkv.bias"])
-        assert_tight(y, O.qmm_f64_bf16w(x, ref["wq"], ref["scales_bf16"], ref["biases_bf16"], 64,
+        assert_tight(y, O.qmm_f64_bf16w(x, ref["wq"], ref["scales_bf16"], ref["biases_bf16"], gs,
                                         bits, bias=bias), "converted layer")
 
 

@@ -12,8 +12,7 @@ import pytest
 import torch
 
 import wuxianhuabu_amd as mx
-from tests.gpu_util import (assert_tight, dev_bf16, dev_words, host_bf16, host_f32_of_bf16,
-                            host_words, spec_metric)
+from tests.gpu_util import assert_tight, dev_bf16, dev_words, host_f32_of_bf16, spec_metric
 from tests.test_gpu_matmul import make_case
 
 pytestmark = pytest.mark.gpu

@@ -2,7 +2,6 @@
 hipMemcpyAsync): bytes equal the file's across chunk boundaries and back-to-back reads
 that reuse the staging buffers, and modules loaded from a file equal the same modules
 built from the tensors in memory."""
-import numpy as np
 import pytest
 import torch
 from safetensors.torch import save_file
