@@ -162,9 +162,11 @@ int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
 /* ---- tiled weight layout ----------------------------------------------------
  * A load-time reordering of the same packed bits (no requantization) in which
  * every weight load of both kernels is a coalesced 16-byte-per-lane access:
- * records of (64 output rows x 64 codes) in row-block-major order, each record
- * holding the codes in lane order followed by one (scale, bias) bf16 pair per
- * lane unit. Rows past N are zero. Requires K % 64 == 0 and bf16 scales/biases.
+ * records of (64 output rows x 64 codes) in step-major order (the records of one
+ * 64-code K step, all row blocks, are adjacent), each record holding the codes in
+ * lane order followed by one (scale, bias) bf16 pair per lane unit. Rows past N
+ * are zero. Requires K % 64 == 0 and bf16 scales/biases; the tiled copy stays
+ * below 2 GiB (mxq_tiled_bytes is MXQ_ERR_INVALID above).
  * The MLX-layout entry points above remain the drop-in operators; the tiled
  * ones are what QuantizedLinear uses once its weights are resident (the
  * reference keeps weights resident the same way: H3Weights / MfLinear.load,
@@ -172,7 +174,7 @@ int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
  * for the layout itself. */
 
 /* Bytes needed for the tiled copy of an N x K weight; negative on invalid
- * arguments (then mxq_last_error() says why). */
+ * arguments or a copy of 2 GiB or more (then mxq_last_error() says why). */
 int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits);
 
 /* MLX layout (wq, scales, biases; bf16 scales/biases) -> tiled layout. */

@@ -186,7 +186,7 @@ int orc_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
   int64_t total = orc_tiled_bytes(N, K, gs, bits);
   if (total < 0) return -1;
   memset(out, 0, (size_t)total);
-  const int64_t nk = K / 64, W = K * bits / 32, G = K / gs;
+  const int64_t W = K * bits / 32, G = K / gs;
   const int64_t rec = 512 * (int64_t)bits + 256 * (gs == 32 ? 2 : 1);
   const int gps = gs == 32 ? 2 : 1;
   for (int64_t n = 0; n < N; ++n) {
@@ -196,7 +196,7 @@ int orc_tile(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
       const int64_t kk = k / 64;
       const int g = (int)((k % 64) / 32);
       const int u = r + 32 * g;
-      uint8_t* R = out + (rb * nk + kk) * rec;
+      uint8_t* R = out + (kk * ((N + 63) / 64) + rb) * rec; /* step-major records */
       uint32_t q = code_at(wq + n * W, k, bits);
       for (int t = 0; t < bits; ++t) {
         int pos = (int)(k % 32) * bits + t; /* bit position in the unit's run */

@@ -20,7 +20,8 @@ def untile(buf, N, K, gs, bits):
     Npad = 64 * ceil(N/64): padding rows come back too, so callers can check
     they are zero."""
     RB, nk, rec, gps = geometry(N, K, gs, bits)
-    T = np.asarray(buf, np.uint8).reshape(RB, nk, rec)
+    # records are step-major: record (rb, kk) at (kk * RB + rb) * rec
+    T = np.asarray(buf, np.uint8).reshape(nk, RB, rec).transpose(1, 0, 2)
     FP, RW = bits // 4, bits % 4
     codes = T[:, :, :512 * bits].reshape(RB, nk, 2, 256 * bits)
     parts = []

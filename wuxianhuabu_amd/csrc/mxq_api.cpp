@@ -6,7 +6,7 @@
 // names the mlx operation it stands in for, as mlx's own messages do
 // ("[quantize] ...", "[quantized_matmul] ..."). The reference reaches these
 // checks through MLX-Swift (`model/minimax h3/H3Common.swift:358-359`).
-// Nothing here allocates device memory.
+// Nothing here allocates device memory but mxq_malloc (for hosts without HIP).
 #include "../../include/mxq.h"
 
 #include <hip/hip_runtime.h>
@@ -323,6 +323,9 @@ int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits) {
   if (rc) return rc;
   if (N < 0) return fail(MXQ_ERR_INVALID, "[tile] N must be non-negative.");
   if (!fits(N, K)) return fail(MXQ_ERR_INVALID, "[tile] N x K out of range.");
+  if (K % 64 == 0 &&
+      mxq::tiled::total_bytes(N, K, group_size, bits) > mxq::tiled::kMaxTiledBytes)
+    return fail(MXQ_ERR_INVALID, "[tile] A tiled weight above 2 GiB is not supported.");
   if (K % 64 != 0)
     return fail(MXQ_ERR_INVALID,
                 "[tile] The tiled layout needs K to be a multiple of 64 (got %lld).",
@@ -412,10 +415,8 @@ int check_tiled(const char* op, const void* x, int64_t M, int64_t K, const void*
   if (K > kMaxK)
     return fail(MXQ_ERR_INVALID, "[%s] K above 2^22 (%lld) is not supported (got %lld).", op,
                 static_cast<long long>(kMaxK), static_cast<long long>(K));
-  if (mxq::tiled::total_bytes(N, K, gs, bits) / mxq::tiled::row_blocks(N == 0 ? 1 : N) >
-      INT32_MAX)
-    return fail(MXQ_ERR_INVALID, "[%s] K too large for one row block (%lld).", op,
-                static_cast<long long>(K));
+  if (mxq::tiled::total_bytes(N, K, gs, bits) > mxq::tiled::kMaxTiledBytes)
+    return fail(MXQ_ERR_INVALID, "[%s] A tiled weight above 2 GiB is not supported.", op);
   if (M == 0 || N == 0) return MXQ_OK;
   if (!x || !tiled || !y) return fail(MXQ_ERR_NULL, "[%s] x, tiled and y must be non-NULL.", op);
   if (!aligned4(x) || !aligned4(y) || (bias && !aligned4(bias)) ||
@@ -523,7 +524,8 @@ int64_t mxq_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int
   // MFMA kernels accumulate each output in the same order: the result bits are the same.
   constexpr int64_t kTileMinM = 1024;
   if (M < kTileMinM || M > INT32_MAX || N == 0 || N > INT32_MAX || K == 0 || K % 64 != 0 ||
-      K > kMaxK || !mxq::detail::qmm_supports_bits(bits))
+      K > kMaxK || !mxq::detail::qmm_supports_bits(bits) ||
+      mxq::tiled::total_bytes(N, K, group_size, bits) > mxq::tiled::kMaxTiledBytes)
     return 0;
   return mxq::tiled::total_bytes(N, K, group_size, bits);
 }

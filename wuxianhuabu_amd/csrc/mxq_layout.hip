@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
   if (idx >= items) return;
   const int u = static_cast<int>(idx & 63);
   const int h = static_cast<int>((idx >> 6) & 1);
-  const int64_t rk = idx >> 7;  // rb * nk + kk
+  const int64_t rk = idx >> 7;  // rb * nk + kk (thread order; the record is step-major)
   const int64_t rb = rk / nk, kk = rk - rb * nk;
   const int r = u & 31, g = u >> 5;
   // source row of tiled row rb*64 + h*32 + r; with `pairs`, the halves of row
@@ -200,7 +200,8 @@ __global__ __launch_bounds__(kThreads) void tile_kernel(const uint32_t* __restri
 #pragma unroll
     for (int i = 0; i < RW; ++i) words[4 * FP + i] = valid ? src[4 * FP + i] : 0u;
   }
-  uint8_t* rec = out + rk * tiled::record_bytes(BITS, gs);
+  uint8_t* rec = out + tiled::record_index(rb, kk, tiled::row_blocks(N)) *
+                           tiled::record_bytes(BITS, gs);
   uint8_t* half = rec + h * tiled::half_bytes(BITS);
   // one 16-byte store per plane (a wave writes 1 KiB of a plane contiguously); the
   // remainder plane holds RW words per unit
@@ -289,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void tile_rows_kernel(const uint32_t* __r
     const uint32_t* sw = reinterpret_cast<const uint32_t*>(st + t * RSTR + (2 * ks + g) * BITS * 4);
 #pragma unroll
     for (int i = 0; i < BITS; ++i) words[i] = sw[i];
-    const int64_t rk = rb * nk + kk;
-    uint8_t* rec = out + rk * tiled::record_bytes(BITS, gs);
+    uint8_t* rec = out + tiled::record_index(rb, kk, tiled::row_blocks(N)) *
+                             tiled::record_bytes(BITS, gs);
     uint8_t* half = rec + h * tiled::half_bytes(BITS);
 #pragma unroll
     for (int p = 0; p < FP; ++p)
@@ -353,7 +354,8 @@ __global__ __launch_bounds__(kThreads) void untile_rows_kernel(const uint8_t* __
     const int64_t kk = k0 + ks;
     if (kk >= nk) continue;
     const int r = u & 31, g = u >> 5, t = h * 32 + r;
-    const uint8_t* rec = in + (rb * nk + kk) * tiled::record_bytes(BITS, gs);
+    const uint8_t* rec = in + tiled::record_index(rb, kk, tiled::row_blocks(N)) *
+                                  tiled::record_bytes(BITS, gs);
     const uint8_t* half = rec + h * tiled::half_bytes(BITS);
     uint32_t words[BITS];
 #pragma unroll

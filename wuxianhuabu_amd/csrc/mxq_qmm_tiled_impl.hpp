@@ -150,11 +150,13 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
                            static_cast<uint32_t>(min(BM, M - m0)) * K * 2);
   };
   // this wave's row block of one feature tile (clamped: a block past N computes
-  // rows that are never stored)
+  // rows that are never stored), from its step-0 record to the end of the layout;
+  // step kk's record lies kk * step_bytes further (records are step-major)
+  const int step_bytes = row_blocks * R::BYTES;
   auto w_rsrc = [&](int n0) {
     const int rb = min((n0 >> 6) + wave, row_blocks - 1);
-    return ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * R::BYTES,
-                           static_cast<uint32_t>(nk) * R::BYTES);
+    return ring::make_rsrc(tw + static_cast<int64_t>(rb) * R::BYTES,
+                           static_cast<uint32_t>(nk * row_blocks - rb) * R::BYTES);
   };
 
   // activation request i of this wave fills stage rows (wave*XL + i)*8 .. +8:
@@ -220,10 +222,10 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_tiled_kernel(
       const int j = i - XL;
       const uint8_t* dst = wl + st * WSTAGE + wave * R::BYTES;
       if (j < R::CHUNKS) {
-        ring::lds_load<16>(wr, dst + j * 1024, lane * 16, kw * R::BYTES + j * 1024);
+        ring::lds_load<16>(wr, dst + j * 1024, lane * 16, kw * step_bytes + j * 1024);
       } else {
         const int off = R::CHUNKS * 1024 + (j - R::CHUNKS) * 256;
-        ring::lds_load<4>(wr, dst + off, lane * 4, kw * R::BYTES + off);
+        ring::lds_load<4>(wr, dst + off, lane * 4, kw * step_bytes + off);
       }
     }
   };

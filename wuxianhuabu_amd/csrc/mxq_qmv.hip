@@ -340,7 +340,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // of the batch: cro = its row's offset, cco = the chunk's, clo = where it is staged
   // packed as (row within the half) | (chunk << 8), unpacked where used
   int tcq[MLX ? NCL : 1];
-  int rows = 0, rowb = 0;
+  int rows = 0, rowb = 0, step_bytes = 0;
   if constexpr (MLX) {
     rowb = K / 8 * BITS;                                // bytes per weight row
     const int G = GP == 2 ? K >> 5 : K >> (6 + gshift);  // groups per row
@@ -363,7 +363,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
       tcq[i] = (q / CPR) | ((q % CPR) << 8);
     }
   } else {
-    wrs = ring::make_rsrc(tw + static_cast<int64_t>(rb) * nk * RB, static_cast<uint32_t>(nk) * RB);
+    // from the row block's step-0 record to the end of the layout (step-major records)
+    const int rbs = (N + 63) >> 6;
+    wrs = ring::make_rsrc(tw + static_cast<int64_t>(rb) * RB,
+                          static_cast<uint32_t>(nk * rbs - rb) * RB);
+    step_bytes = rbs * RB;
     srs = brs = wrs;
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb) {
@@ -460,7 +464,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     for (int j = 0; j < SPW; ++j) {
       // uniform, kept in an SGPR (a VGPR soffset would become a readfirstlane loop)
       const int kj = min(b0 + j, k_end - 1);
-      const int so = __builtin_amdgcn_readfirstlane(MLX ? kj * 8 * BITS : kj * RB);
+      const int so = __builtin_amdgcn_readfirstlane(MLX ? kj * 8 * BITS : kj * step_bytes);
 #pragma unroll
       for (int nb = 0; nb < NH; ++nb) {
         if constexpr (!MLX) {

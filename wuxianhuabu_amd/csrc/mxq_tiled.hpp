@@ -7,7 +7,9 @@
 // weight load of both kernels is a fully coalesced 16-byte-per-lane access:
 //
 //   record (rb, kk) for row block rb = rows [64*rb, 64*rb+64) and K step kk =
-//   codes [64*kk, 64*kk+64), stored at byte (rb * nk + kk) * record_bytes:
+//   codes [64*kk, 64*kk+64), stored at byte (kk * row_blocks + rb) * record_bytes
+//   (step-major: the records of one K step, all row blocks, are adjacent, so the
+//   GEMV's waves, which all start at the same K steps, read neighbouring bytes):
 //     codes, 512*bits bytes: two halves h (rows 64*rb + 32*h + r, r < 32); in
 //       each half, "units" u = 0..63 with row r = u % 32 and code half
 //       g = u / 32 (codes [64*kk + 32*g, +32), i.e. `bits` whole words of the
@@ -19,7 +21,8 @@
 //       in the low half and bf16 bias in the high half, for the group that
 //       holds unit (h, r, g)'s codes.
 //   Rows past N are zero (codes, scale and bias).
-// Requires K % 64 == 0.
+// Requires K % 64 == 0; the whole layout stays below 2 GiB (the kernels' 32-bit
+// step offsets).
 #pragma once
 
 #include <stdint.h>
@@ -40,6 +43,11 @@ __host__ __device__ inline int64_t row_blocks(int64_t N) { return (N + 63) / 64;
 __host__ __device__ inline int64_t total_bytes(int64_t N, int64_t K, int gs, int bits) {
   return row_blocks(N) * (K / 64) * static_cast<int64_t>(record_bytes(bits, gs));
 }
+// record index of (row block rb, K step kk) among rbs = row_blocks(N)
+__host__ __device__ inline int64_t record_index(int64_t rb, int64_t kk, int64_t rbs) {
+  return kk * rbs + rb;
+}
+constexpr int64_t kMaxTiledBytes = 0x7FFFFFFF;
 
 }  // namespace tiled
 }  // namespace mxq
