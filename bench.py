@@ -461,6 +461,20 @@ def main():
             "workspace_bytes": ws.numel(), "note": "mxq_quantized_matmul_ws: mxq_tile + tiled qmm"}
         print(f"[bench] qmm (MLX layout, workspace): avg {wavg:.3f} ms", file=sys.stderr, flush=True)
         del ws
+
+        # the drop-in call itself: its workspace comes from the library's stream-ordered pool
+        def qmm_dropin_launch(_i):
+            ok(L.mxq_quantized_matmul(P(x), c["M"], c["K"], P(wq), P(s), P(b), c["N"], 1, c["gs"],
+                                      c["bits"], None, P(y), cur()))
+
+        dper_, _ = time_launches(torch, qmm_dropin_launch, max(5, steps // 3), 2)
+        davg = sum(dper_) / len(dper_)
+        res["qmm_dropin"] = {
+            "ms": davg, "tflops": 2.0 * c["M"] * c["N"] * c["K"] / (davg * 1e-3) / 1e12,
+            "note": "mxq_quantized_matmul on the MLX layout: pooled stream-ordered workspace, "
+                    "mxq_tile + tiled qmm"}
+        print(f"[bench] qmm (drop-in, pooled workspace): avg {davg:.3f} ms", file=sys.stderr,
+              flush=True)
     per, total = time_launches(torch, qmm_launch, steps, warmup)
     flop = 2.0 * c["M"] * c["N"] * c["K"]
     per_sorted = sorted(per)

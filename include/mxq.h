@@ -35,7 +35,8 @@
  *   - All tensor pointers are DEVICE pointers, row-major and contiguous,
  *     owned by the caller. Functions enqueue on `stream` (a hipStream_t;
  *     NULL = the default stream) and return without synchronising.
- *   - No function allocates device memory, except mxq_malloc (below).
+ *   - No function allocates device memory, except mxq_malloc (below) and the
+ *     stream-ordered workspace of a large-M mxq_quantized_matmul call (there).
  *   - Packed layout: for output row n, code k occupies bits [k*bits, k*bits+bits)
  *     of the little-endian bitstream formed by wq[n, 0..K*bits/32).
  *     scales, biases: [rows, K/group_size]; w = q*scale + bias.
@@ -107,8 +108,16 @@ int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t
  * scales/biases bf16 [N, K/group_size]; fp32 accumulation; bias may be NULL.
  * transpose must be 1 (the only form the reference uses,
  * `model/minimax h3/H3Common.swift:358-359`); transpose == 0 returns
- * MXQ_ERR_UNSUPPORTED. M <= MXQ_QMV_MAX_M runs the GEMV kernel, larger M the
- * MFMA kernel. M == 0 or N == 0 is a no-op. */
+ * MXQ_ERR_UNSUPPORTED. M <= MXQ_QMV_MAX_M runs the GEMV kernel, larger M an MFMA
+ * kernel. M == 0 or N == 0 is a no-op.
+ * When mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits) is positive, the
+ * call takes that many bytes of stream-ordered workspace from a memory pool the library
+ * owns (one per GPU, created on first use, kept until the process ends, caching up to
+ * 256 MiB of freed workspace), tiles the weight into it, runs the tiled MFMA kernel and
+ * frees the workspace on `stream`: mxq_quantized_matmul_ws with a workspace of its own,
+ * the same result bits as the in-place kernel. On a stream under graph capture, or where
+ * the pool cannot supply the bytes, it runs the in-place MFMA kernel and allocates
+ * nothing. */
 int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,
                          const void* scales, const void* biases, int64_t N, int transpose,
                          int group_size, int bits, const void* bias, void* y,
@@ -121,7 +130,8 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
  * workspace holds that many bytes (16-byte aligned), the weight is first tiled into it
  * (mxq_tile) and the tiled MFMA kernel runs: bit-identical results, about 1.6x faster
  * at M = 14400, K = 4096, N = 16384. Otherwise, including a NULL or too small
- * workspace, this is mxq_quantized_matmul. Allocates nothing; the workspace is
+ * workspace, this is mxq_quantized_matmul's in-place form (the GEMV or the in-place
+ * MFMA kernel). Allocates nothing; the workspace is
  * overwritten, and calls sharing one workspace must be ordered on one stream. A
  * workspace that overlaps x, the weight triple, bias or y is MXQ_ERR_INVALID.
  * The size is positive only for M >= 1024 and K % 64 == 0; a negative return is an
@@ -140,7 +150,8 @@ int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t*
  * and nothing is freed. When the tiled path applies (workspace_size > 0) and the
  * tiled weight fits, the weight is tiled into that array and the tiled kernel runs
  * (the same result bits as mxq_quantized_matmul); when it does not apply, this is
- * mxq_quantized_matmul; a tiled weight above the array's size is MXQ_ERR_INVALID.
+ * mxq_quantized_matmul's in-place form (nothing allocated); a tiled weight above the
+ * array's size is MXQ_ERR_INVALID.
  * Every call on one GPU shares that GPU's array: calls that may overlap on one GPU
  * (different streams, not ordered) race and must be serialised by the caller. */
 #define MXQ_NOALLOC_SCRATCH_BYTES (64ll << 20)

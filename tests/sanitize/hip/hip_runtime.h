@@ -75,6 +75,48 @@ inline hipError_t hipStreamGetDevice(hipStream_t, int* d) {
   *d = 0;
   return hipSuccess;
 }
+inline hipError_t hipGetLastError() { return hipSuccess; }
+// stream-ordered allocation from a pool: host memory here, refused above 64 MiB so the
+// fallback to the in-place kernel is exercised too
+typedef struct ihipMemPool_t* hipMemPool_t;
+enum hipMemAllocationType { hipMemAllocationTypeInvalid = 0, hipMemAllocationTypePinned = 1 };
+enum hipMemAllocationHandleType { hipMemHandleTypeNone = 0 };
+enum hipMemLocationType { hipMemLocationTypeInvalid = 0, hipMemLocationTypeDevice = 1 };
+struct hipMemLocation { hipMemLocationType type; int id; };
+struct hipMemPoolProps {
+  hipMemAllocationType allocType;
+  hipMemAllocationHandleType handleTypes;
+  hipMemLocation location;
+  void* win32SecurityAttributes;
+  size_t maxSize;
+  unsigned char reserved[56];
+};
+enum hipMemPoolAttr { hipMemPoolAttrReleaseThreshold = 4 };
+enum hipDeviceAttribute_t { hipDeviceAttributeMemoryPoolsSupported = 1 };
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+  *v = 1;
+  return hipSuccess;
+}
+inline hipError_t hipMemPoolCreate(hipMemPool_t* p, const hipMemPoolProps*) {
+  *p = reinterpret_cast<hipMemPool_t>(std::malloc(1));
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipMemPoolSetAttribute(hipMemPool_t, hipMemPoolAttr, void*) {
+  return hipSuccess;
+}
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* c) {
+  *c = hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+inline hipError_t hipMallocFromPoolAsync(void** p, size_t n, hipMemPool_t, hipStream_t) {
+  *p = n <= (size_t(64) << 20) ? std::malloc(n) : nullptr;
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+inline hipError_t hipFreeAsync(void* p, hipStream_t) {
+  std::free(p);
+  return hipSuccess;
+}
 template <typename T>
 inline hipError_t hipGetSymbolAddress(void** p, const T* symbol) {
   *p = const_cast<void*>(static_cast<const void*>(symbol));
