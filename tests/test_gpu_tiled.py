@@ -193,9 +193,13 @@ def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
     MLX layout in place: same wave split, same per-step arithmetic, so the
     outputs agree bit for bit (ragged N, every token count). K = 192 gives rows
     of 24 * bits bytes, not whole 16-byte chunks for odd widths: the batch's
-    coalesced loads then straddle row ends."""
+    coalesced loads then straddle row ends. The MLX form loads each batch's scales and
+    biases as one window per row: K = 320 (5 groups of 64 per row, so the window's
+    alignment differs between rows), 2688 and 1856 (waves whose batches start at odd
+    steps, gs = 128 groups split between batches), 3840 (the Gemma-4 logits K)."""
     for (M, N, K) in [(1, 200, 1024), (2, 200, 1024), (3, 200, 1024), (5, 200, 1024),
-                      (8, 200, 1024), (2, 130, 192), (7, 130, 192)]:
+                      (8, 200, 1024), (2, 130, 192), (7, 130, 192), (1, 130, 320),
+                      (2, 200, 2688), (5, 70, 1856), (3, 300, 3840)]:
         if K % gs:
             continue
         x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 17 + gs + M,

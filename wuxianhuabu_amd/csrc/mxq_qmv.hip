@@ -283,7 +283,11 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // LDS region, and lane (l32, g2) reads back the BITS words of codes
 // [64k + 32 g2, +32) of its row l32 (a run of 32 codes is BITS whole words);
 // it loads that row's scale and bias of step k's group(s) itself. Everything
-// else is shared. gshift = log2(gs / 64) for gs >= 64.
+// else is shared. gshift = log2(gs / 64) for gs >= 64. With batches of 4 steps, a lane
+// loads its row's scales (and biases) of the whole batch at once: a dword-aligned window
+// of 12 bytes (16 for gs = 32) holding the batch's groups, split where used. A row's
+// scales for all of K lie in one or two 128-byte lines, which one 2-byte load per step
+// asked L2 for once per step.
 template <int BITS, int MT, int GP, int NH, int WPB, int SPW, bool MLX>
 __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
@@ -487,7 +491,9 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           }
         }
         if constexpr (MLX) {
-          if constexpr (GP == 2) {  // groups 2k and 2k + 1
+          if constexpr (SPW == 4) {
+            // whole-batch windows, below
+          } else if constexpr (GP == 2) {  // groups 2k and 2k + 1
             const int ss = __builtin_amdgcn_readfirstlane(kj * 4);
             B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(srs, svo[nb], ss, kWeightAux);
             B.sb[j][nb][1] = __builtin_amdgcn_raw_buffer_load_b32(brs, svo[nb], ss, kWeightAux);
@@ -502,6 +508,32 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           B.sb[j][nb][GP - 1] = v.y;
         } else {
           B.sb[j][nb][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, svo[nb], so, kWeightAux);
+        }
+      }
+    }
+    if constexpr (MLX && SPW == 4) {
+      // the batch's scales and biases of the lane's row, one window each; the whole
+      // offset is in the vector offset, which the range check covers (past the last
+      // row: zeros, never used). GP == 2: dword j = groups 2(b0+j), 2(b0+j)+1, as one
+      // load per step gives them. GP == 1: three dwords from the even halfword at or
+      // below the batch's first group, b0 >> gshift (sb[0..2][nb]).
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) {
+        if constexpr (GP == 2) {
+          const v4u_t sv = __builtin_amdgcn_raw_buffer_load_b128(srs, svo[nb] + 4 * b0, 0,
+                                                                 kWeightAux);
+          const v4u_t bv = __builtin_amdgcn_raw_buffer_load_b128(brs, svo[nb] + 4 * b0, 0,
+                                                                 kWeightAux);
+          B.sb[0][nb][0] = sv.x; B.sb[1][nb][0] = sv.y; B.sb[2][nb][0] = sv.z;
+          B.sb[3][nb][0] = sv.w;
+          B.sb[0][nb][1] = bv.x; B.sb[1][nb][1] = bv.y; B.sb[2][nb][1] = bv.z;
+          B.sb[3][nb][1] = bv.w;
+        } else {
+          const int a = (((svo[nb] >> 1) + (b0 >> gshift)) & ~1) * 2;
+          const v3u_t sv = __builtin_amdgcn_raw_buffer_load_b96(srs, a, 0, kWeightAux);
+          const v3u_t bv = __builtin_amdgcn_raw_buffer_load_b96(brs, a, 0, kWeightAux);
+          B.sb[0][nb][0] = sv.x; B.sb[1][nb][0] = sv.y; B.sb[2][nb][0] = sv.z;
+          B.sb[0][nb][1] = bv.x; B.sb[1][nb][1] = bv.y; B.sb[2][nb][1] = bv.z;
         }
       }
     }
@@ -600,7 +632,22 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
                                                         0, 0, 0);
           float sc, bi;
           if constexpr (MLX) {
-            const uint32_t sv = B.sb[j][nb][0], bv2 = B.sb[j][nb][1];
+            uint32_t sv = B.sb[j][nb][0], bv2 = B.sb[j][nb][1];
+            if constexpr (GP == 1 && SPW == 4) {
+              // halfword h of the window: group (b0 + j) >> gshift, counted from the
+              // window's first (even) halfword
+              const int hw0 = (svo[nb] >> 1) + (b0 >> gshift);
+              const int h = ((b0 + j) >> gshift) - (b0 >> gshift) + (hw0 & 1);
+              const int d = h >> 1;
+              // values, not lvalues: a choice between elements would index the batch
+              // at run time and move it to scratch memory
+              const uint32_t s0 = B.sb[0][nb][0], s1 = B.sb[1][nb][0], s2 = B.sb[2][nb][0];
+              const uint32_t c0 = B.sb[0][nb][1], c1 = B.sb[1][nb][1], c2 = B.sb[2][nb][1];
+              const uint32_t ws = d == 0 ? s0 : d == 1 ? s1 : s2;
+              const uint32_t wb = d == 0 ? c0 : d == 1 ? c1 : c2;
+              sv = (h & 1) ? ws >> 16 : ws;
+              bv2 = (h & 1) ? wb >> 16 : wb;
+            }
             sc = __uint_as_float(e ? sv & 0xFFFF0000u : sv << 16);
             bi = __uint_as_float(e ? bv2 & 0xFFFF0000u : bv2 << 16);
           } else {
