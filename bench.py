@@ -219,58 +219,67 @@ def cpu_leg(results, bufs, qmm_c, gemv_c, budget_s, checks=()):
     if checks:
         out["extra_checks"] = extra_checks
 
-    # -- CPU baseline: mlx CPU qmm loop structure, bf16 arithmetic, 1 core --
+    # -- CPU baseline: mlx CPU qmm loop structure, bf16 arithmetic, 1 core. Timed with
+    # the oracle compiled for this host (-march=native) where gcc is here, else with the
+    # prebuilt x86-64-v3 library --
     K, N = qmm_c["K"], qmm_c["N"]
+    NL = O.native_lib()
+    build = ("gcc " + " ".join(O.NATIVE_FLAGS) + ", compiled on this host" if NL is not None
+             else "prebuilt oracle/libmxq_oracle.so (gcc -O3 -march=x86-64-v3)")
     t0 = time.perf_counter()
-    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=1)
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=1,
+                  L=NL)
     t_row = time.perf_counter() - t0
     nrows = int(max(1, min(64, budget_s / max(t_row, 1e-3))))
     sample = np.arange(nrows, dtype=np.int64)
     t0 = time.perf_counter()
-    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=sample, threads=1)
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=sample, threads=1,
+                  L=NL)
     t = time.perf_counter() - t0
     flops = 2.0 * nrows * N * K
     out["cpu_baseline"] = {
-        "value": flops / t / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+        "value": flops / t / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port", "build": build,
         "sample": f"{nrows} of {qmm_c['M']} rows of the qmm workload (mlx CPU qmm loop "
                   f"restated in C, bf16 arithmetic), {t:.1f} s; the loop is linear in M",
     }
     # the same loop with an fp32 running sum and fp32 products (the variant BASELINE
     # times beside the bf16 one), 1 core, a third of the budget
     t0 = time.perf_counter()
-    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=1, rows=[0], threads=1)
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=1, rows=[0], threads=1,
+                  L=NL)
     t_row = time.perf_counter() - t0
     nrows32 = int(max(1, min(256, budget_s / 3 / max(t_row, 1e-3))))
     t0 = time.perf_counter()
     O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=1,
-                  rows=np.arange(nrows32, dtype=np.int64), threads=1)
+                  rows=np.arange(nrows32, dtype=np.int64), threads=1, L=NL)
     t32 = time.perf_counter() - t0
     out["cpu_baseline_fp32acc"] = {
         "value": 2.0 * nrows32 * N * K / t32 / 1e12, "unit": "TFLOP/s", "cores": 1,
-        "kind": "port",
+        "kind": "port", "build": build,
         "sample": f"{nrows32} of {qmm_c['M']} rows, {t32:.1f} s, fp32 products and sum"}
     # the same loop over all host cores this process may use (OpenMP over N), on a
     # sample sized to the same budget
     nthr = threads
     t0 = time.perf_counter()
-    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=nthr)
+    O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0, rows=[0], threads=nthr,
+                  L=NL)
     t_row = time.perf_counter() - t0
     nrows_mc = int(max(1, min(256, budget_s / 2 / max(t_row, 1e-3))))
     t0 = time.perf_counter()
     O.qmm_mlx_cpu(xh, wqh, sh, bh, qmm_c["gs"], qmm_c["bits"], accum=0,
-                  rows=np.arange(nrows_mc, dtype=np.int64), threads=nthr)
+                  rows=np.arange(nrows_mc, dtype=np.int64), threads=nthr, L=NL)
     tmc = time.perf_counter() - t0
     out["cpu_baseline_all_cores"] = {
         "value": 2.0 * nrows_mc * N * K / tmc / 1e12, "unit": "TFLOP/s", "cores": nthr,
-        "kind": "port",
+        "kind": "port", "build": build,
         "sample": f"{nrows_mc} of {qmm_c['M']} rows, {tmc:.1f} s, OpenMP over N"}
     # GEMV on the CPU: the full M=2 workload, 1 core
     t0 = time.perf_counter()
     O.qmm_mlx_cpu(host_u16(gx), host_u32(gwq), host_u16(gs_), host_u16(gb), gemv_c["gs"],
-                  gemv_c["bits"], accum=0, threads=1)
+                  gemv_c["bits"], accum=0, threads=1, L=NL)
     tg = time.perf_counter() - t0
     out["cpu_baseline_gemv"] = {"value": gemv_bytes(gemv_c) / tg / 1e9, "unit": "GB/s",
-                                "cores": 1, "kind": "port",
+                                "cores": 1, "kind": "port", "build": build,
                                 "sample": f"full M=2 workload, {tg:.2f} s"}
     try:
         with open("/proc/cpuinfo") as f:

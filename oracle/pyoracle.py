@@ -7,6 +7,7 @@ never imports this module.
 import ctypes
 import os
 import subprocess
+import tempfile
 
 import numpy as np
 
@@ -35,7 +36,33 @@ def lib():
         return _lib
     if not os.path.exists(LIB_PATH):
         build()
-    L = ctypes.CDLL(LIB_PATH)
+    _lib = _bind(ctypes.CDLL(LIB_PATH))
+    return _lib
+
+
+_native = None
+NATIVE_FLAGS = ["-O3", "-march=native", "-fopenmp", "-fPIC", "-std=c11"]
+
+
+def native_lib():
+    """The oracle compiled for the CPU this process runs on (gcc with NATIVE_FLAGS, into
+    a temporary directory), for the CPU baseline's timing; None where gcc is missing or
+    the build fails (the caller then times the prebuilt x86-64-v3 library)."""
+    global _native
+    if _native is None:
+        try:
+            out = os.path.join(tempfile.mkdtemp(prefix="mxq_oracle_native_"),
+                               "libmxq_oracle_native.so")
+            subprocess.run(["gcc", *NATIVE_FLAGS, "-shared", "-o", out,
+                            os.path.join(HERE, "mxq_oracle.c"), "-lm"],
+                           check=True, capture_output=True, timeout=120)
+            _native = _bind(ctypes.CDLL(out))
+        except (OSError, subprocess.SubprocessError):
+            _native = False
+    return _native or None
+
+
+def _bind(L):
     L.orc_version.restype = _int
     L.orc_splitmix64_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     L.orc_splitmix64_next.restype = ctypes.c_uint64
@@ -69,7 +96,6 @@ def lib():
     L.orc_tiled_bytes.restype = _i64
     L.orc_tile.argtypes = [_u32p, _u16p, _u16p, _i64, _i64, _int, _int, _u8p]
     L.orc_tile.restype = _int
-    _lib = L
     return L
 
 
@@ -211,7 +237,9 @@ def qmm_f64_bf16w(x, wq, scales, biases, gs, bits, bias=None, rows=None, threads
     return _qmm64(lib().orc_qmm_f64_bf16w, x, wq, scales, biases, gs, bits, bias, rows, threads)
 
 
-def qmm_mlx_cpu(x, wq, scales, biases, gs, bits, accum=0, rows=None, threads=1):
+def qmm_mlx_cpu(x, wq, scales, biases, gs, bits, accum=0, rows=None, threads=1, L=None):
+    """L: the library to run (default the prebuilt oracle; native_lib() for timing)."""
+    L = L or lib()
     x = _c(x, np.uint16)
     wq = _c(wq, np.uint32)
     M, K = x.shape
@@ -219,8 +247,8 @@ def qmm_mlx_cpu(x, wq, scales, biases, gs, bits, accum=0, rows=None, threads=1):
     rp, nr, keep = _rows_arg(rows)
     nrows = M if rows is None else nr
     y = np.empty((nrows, N), np.uint16)
-    _check(lib().orc_qmm_mlx_cpu(x, M, K, wq, _c(scales, np.uint16), _c(biases, np.uint16), N,
-                                 gs, bits, accum, rp, nr, threads, y), "qmm_mlx_cpu")
+    _check(L.orc_qmm_mlx_cpu(x, M, K, wq, _c(scales, np.uint16), _c(biases, np.uint16), N,
+                             gs, bits, accum, rp, nr, threads, y), "qmm_mlx_cpu")
     del keep
     return y
 
