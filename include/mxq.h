@@ -36,7 +36,7 @@
  *     owned by the caller. Functions enqueue on `stream` (a hipStream_t;
  *     NULL = the default stream) and return without synchronising.
  *   - No function allocates device memory, except mxq_malloc (below) and the
- *     stream-ordered workspace of a large-M mxq_quantized_matmul call (there).
+ *     stream-ordered workspace of an MFMA-path mxq_quantized_matmul call (there).
  *   - Packed layout: for output row n, code k occupies bits [k*bits, k*bits+bits)
  *     of the little-endian bitstream formed by wq[n, 0..K*bits/32).
  *     scales, biases: [rows, K/group_size]; w = q*scale + bias.
@@ -110,14 +110,14 @@ int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t
  * `model/minimax h3/H3Common.swift:358-359`); transpose == 0 returns
  * MXQ_ERR_UNSUPPORTED. M <= MXQ_QMV_MAX_M runs the GEMV kernel, larger M an MFMA
  * kernel. M == 0 or N == 0 is a no-op.
- * When mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits) is positive, the
- * call takes that many bytes of stream-ordered workspace from a memory pool the library
- * owns (one per GPU, created on first use, kept until the process ends, caching up to
- * 256 MiB of freed workspace), tiles the weight into it, runs the tiled MFMA kernel and
- * frees the workspace on `stream`: mxq_quantized_matmul_ws with a workspace of its own,
- * the same result bits as the in-place kernel. On a stream under graph capture, or where
- * the pool cannot supply the bytes, it runs the in-place MFMA kernel and allocates
- * nothing. */
+ * For M > MXQ_QMV_MAX_M with K % 64 == 0 (and a tiled copy below 2 GiB) the call takes
+ * mxq_tiled_bytes(N, K, group_size, bits) bytes of stream-ordered workspace from a memory
+ * pool the library owns (one per GPU, created on first use, kept until the process ends,
+ * caching up to 256 MiB of freed workspace), tiles the weight into it, runs the tiled MFMA
+ * kernel and frees the workspace on `stream`: for 2, 4, 6 and 8 bits the same result bits
+ * as the in-place MFMA kernel (3- and 5-bit codes, whose in-place form is the GEMV
+ * kernel, differ from it in the last bits). On a stream under graph capture, or where the
+ * pool cannot supply the bytes, it runs the in-place kernel and allocates nothing. */
 int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,
                          const void* scales, const void* biases, int64_t N, int transpose,
                          int group_size, int bits, const void* bias, void* y,

@@ -1,8 +1,9 @@
-"""mxq_quantized_matmul at large M on the MLX layout: the weight is tiled into a
-stream-ordered workspace from the library's pool and the tiled kernel runs. Checked
-through the C ABI against the in-place MFMA kernel (mxq_qmm) and the caller-workspace
-entry point (mxq_quantized_matmul_ws), bit for bit, and against the fp64 oracle on
-sampled rows; two streams used at once; under graph capture the call allocates
+"""mxq_quantized_matmul past the GEMV's range (M > 8) on the MLX layout: the weight is
+tiled into a stream-ordered workspace from the library's pool and the tiled kernel runs.
+Checked through the C ABI against the in-place MFMA kernel (mxq_qmm) and the
+caller-workspace entry point (mxq_quantized_matmul_ws), bit for bit, and against the
+fp64 oracle on sampled rows; 3- and 5-bit codes (whose in-place form is the GEMV kernel)
+against the oracle; two streams used at once; under graph capture the call allocates
 nothing (the in-place kernel runs) and every replay gives the same bits.
 """
 import ctypes
@@ -68,6 +69,44 @@ def test_pooled_workspace_matches_in_place_kernel(dev, O, M, N, K, gs, bits):
     assert_tight(host_f32_of_bf16(y)[rows],
                  O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows),
                  f"pooled M={M} N={N} K={K} gs={gs} bits={bits}")
+
+
+@pytest.mark.parametrize("M,N,K,gs,bits", [(9, 512, 1024, 64, 6), (16, 2048, 2048, 64, 4),
+                                           (100, 700, 1536, 32, 8), (300, 1000, 2048, 128, 2),
+                                           (640, 384, 4096, 64, 6)])
+def test_pooled_small_m_matches_in_place_kernel(dev, O, M, N, K, gs, bits):
+    """Below the caller-workspace threshold (M < 1024) the pooled call still tiles."""
+    L = _lib.lib()
+    assert L.mxq_quantized_matmul_workspace_size(M, N, K, gs, bits) == 0
+    host, d = _inputs(O, dev, M, N, K, gs, bits, seed=M * 3 + bits)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    y_in = torch.empty_like(y)
+    assert _plain(L, d, M, N, K, gs, bits, y) == _lib.MXQ_OK, L.mxq_last_error()
+    assert _in_place(L, d, M, N, K, gs, bits, y_in) == _lib.MXQ_OK
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_in), f"pooled vs in-place M={M} N={N} K={K} gs={gs} bits={bits}"
+    x, wq, s, b, bias = host
+    rows = np.unique(np.r_[np.arange(0, M, 7), M - 1])
+    assert_tight(host_f32_of_bf16(y)[rows],
+                 O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows),
+                 f"pooled M={M} N={N} K={K} gs={gs} bits={bits}")
+
+
+@pytest.mark.parametrize("M,bits,gs", [(12, 3, 64), (1100, 5, 32), (300, 3, 128)])
+def test_pooled_3_and_5_bit_codes(dev, O, M, bits, gs):
+    """3- and 5-bit codes: the pooled call runs the tiled MFMA kernel (the in-place form is
+    the GEMV kernel, whose sums differ in the last bits); checked against the oracle."""
+    L = _lib.lib()
+    N, K = 520, 1024
+    host, d = _inputs(O, dev, M, N, K, gs, bits, seed=M + 7 * bits)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    assert _plain(L, d, M, N, K, gs, bits, y) == _lib.MXQ_OK, L.mxq_last_error()
+    torch.cuda.synchronize()
+    x, wq, s, b, bias = host
+    rows = np.unique(np.r_[np.arange(0, M, 11), M - 1])
+    assert_tight(host_f32_of_bf16(y)[rows],
+                 O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows),
+                 f"pooled M={M} bits={bits} gs={gs}")
 
 
 def test_pooled_workspace_two_streams_and_repeated_sizes(dev, O):

@@ -558,6 +558,46 @@ hipMemPool_t workspace_pool(hipStream_t stream) {
   }
   return g_pool[dev];
 }
+
+// Bytes of stream-ordered workspace a large-M mxq_quantized_matmul call tiles the weight
+// into, or 0 where it runs in place: any M past the GEMV's range, K % 64 == 0, a tiled
+// copy below 2 GiB. The tiled kernel takes 0.36-0.95 of the in-place kernel's time,
+// tiling included, from M = 16 (M = 16 to 1024; N x K from 2048 x 2048 to 5376 x 21504,
+// 6-bit), and covers the 3- and 5-bit codes whose in-place form is the GEMV kernel.
+int64_t pooled_workspace_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  if (M <= MXQ_QMV_MAX_M || M > INT32_MAX || N <= 0 || N > INT32_MAX || K <= 0 ||
+      K % 64 != 0 || K > kMaxK || check_bits_gs("quantized_matmul", bits, gs, K) != MXQ_OK)
+    return 0;
+  const int64_t t = mxq::tiled::total_bytes(N, K, gs, bits);
+  return t > mxq::tiled::kMaxTiledBytes ? 0 : t;
+}
+
+// The weight tiled into `workspace` (need bytes, 16-byte aligned, sharing no byte with an
+// operand), then the tiled kernel: mxq_quantized_matmul_ws's work once it has a workspace.
+int matmul_through_workspace(const void* x, int64_t M, int64_t K, const uint32_t* wq,
+                             const void* scales, const void* biases, int64_t N, int group_size,
+                             int bits, const void* bias, void* y, void* workspace, int64_t need,
+                             mxq_stream stream) {
+  int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
+                        bias, y);
+  if (rc) return rc;
+  // the tiler reads the weight triple while it writes the workspace, and the kernel
+  // reads the workspace while it writes y: the workspace may share no byte with them
+  const uintptr_t w0 = reinterpret_cast<uintptr_t>(workspace), w1 = w0 + static_cast<uintptr_t>(need);
+  auto overlaps = [&](const void* p, int64_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return p && bytes > 0 && a < w1 && w0 < a + static_cast<uintptr_t>(bytes);
+  };
+  const int64_t groups = N * (K / group_size);
+  if (overlaps(x, M * K * 2) || overlaps(wq, N * K / 32 * bits * 4) ||
+      overlaps(scales, groups * 2) || overlaps(biases, groups * 2) || overlaps(bias, N * 2) ||
+      overlaps(y, M * N * 2))
+    return fail(MXQ_ERR_INVALID,
+                "[quantized_matmul] The workspace overlaps an input or the output.");
+  rc = mxq_tile(wq, scales, biases, N, K, group_size, bits, workspace, stream);
+  if (rc) return rc;
+  return mxq_qmm_tiled(x, M, K, workspace, N, group_size, bits, bias, y, stream);
+}
 }  // namespace
 
 extern "C" {
@@ -566,12 +606,13 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
                          const void* scales, const void* biases, int64_t N, int transpose,
                          int group_size, int bits, const void* bias, void* y,
                          mxq_stream stream) {
-  // Large M: the weight is tiled into a stream-ordered workspace and the tiled kernel
-  // runs (the same result bits as the in-place kernel, about 1.6x faster at
-  // M = 14400, K = 4096, N = 16384). Invalid arguments are refused before anything is
-  // allocated; where no workspace can be had, the in-place kernel runs.
+  // Past the GEMV's range: the weight is tiled into a stream-ordered workspace and the
+  // tiled kernel runs (for 2, 4, 6 and 8 bits the same result bits as the in-place
+  // kernel; about 1.7x faster at M = 14400, K = 4096, N = 16384 and up to 2.8x at a few
+  // hundred tokens). Invalid arguments are refused before anything is allocated; where no
+  // workspace can be had, the in-place kernel runs.
   if (transpose == 1 && M > MXQ_QMV_MAX_M) {
-    const int64_t need = mxq_quantized_matmul_workspace_size(M, N, K, group_size, bits);
+    const int64_t need = pooled_workspace_bytes(M, N, K, group_size, bits);
     if (need > 0) {
       int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size,
                             bits, bias, y);
@@ -585,8 +626,8 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
       const hipMemPool_t pool = cap == hipStreamCaptureStatusNone ? workspace_pool(s) : nullptr;
       if (pool && hipMallocFromPoolAsync(&ws, static_cast<size_t>(need), pool, s) == hipSuccess &&
           ws) {
-        rc = mxq_quantized_matmul_ws(x, M, K, wq, scales, biases, N, transpose, group_size,
-                                     bits, bias, y, ws, static_cast<size_t>(need), stream);
+        rc = matmul_through_workspace(x, M, K, wq, scales, biases, N, group_size, bits, bias, y,
+                                      ws, need, stream);
         const hipError_t e = hipFreeAsync(ws, s);
         if (rc) return rc;
         return hip_status("quantized_matmul", e);
@@ -624,25 +665,8 @@ int mxq_quantized_matmul_ws(const void* x, int64_t M, int64_t K, const uint32_t*
       (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
     return matmul_in_place(x, M, K, wq, scales, biases, N, transpose, group_size, bits, bias, y,
                            stream);
-  int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size, bits,
-                        bias, y);
-  if (rc) return rc;
-  // the tiler reads the weight triple while it writes the workspace, and the kernel
-  // reads the workspace while it writes y: the workspace may share no byte with them
-  const uintptr_t w0 = reinterpret_cast<uintptr_t>(workspace), w1 = w0 + static_cast<uintptr_t>(need);
-  auto overlaps = [&](const void* p, int64_t bytes) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    return p && bytes > 0 && a < w1 && w0 < a + static_cast<uintptr_t>(bytes);
-  };
-  const int64_t groups = N * (K / group_size);
-  if (overlaps(x, M * K * 2) || overlaps(wq, N * K / 32 * bits * 4) ||
-      overlaps(scales, groups * 2) || overlaps(biases, groups * 2) || overlaps(bias, N * 2) ||
-      overlaps(y, M * N * 2))
-    return fail(MXQ_ERR_INVALID,
-                "[quantized_matmul] The workspace overlaps an input or the output.");
-  rc = mxq_tile(wq, scales, biases, N, K, group_size, bits, workspace, stream);
-  if (rc) return rc;
-  return mxq_qmm_tiled(x, M, K, workspace, N, group_size, bits, bias, y, stream);
+  return matmul_through_workspace(x, M, K, wq, scales, biases, N, group_size, bits, bias, y,
+                                  workspace, need, stream);
 }
 
 }  // extern "C"
