@@ -71,8 +71,9 @@ extern "C" {
 #define MXQ_MODE_MINMAX 0   /* scale=(max-min)/(2^bits-1), bias=min */
 #define MXQ_MODE_MLX_EDGE 1 /* mlx's sign-aware edge quantizer (as recalled) */
 
-/* Largest M served by the GEMV kernel when mxq_quantized_matmul dispatches. */
-#define MXQ_QMV_MAX_M 8
+/* Largest M served by the GEMV kernel when mxq_quantized_matmul dispatches: one pass of
+ * the weight serves up to 32 tokens (K % 64 == 0; other K: passes of 8 tokens). */
+#define MXQ_QMV_MAX_M 32
 
 typedef void* mxq_stream; /* hipStream_t */
 
@@ -108,16 +109,16 @@ int mxq_unpack(const uint32_t* wq, int64_t rows, int64_t cols, int bits, uint8_t
  * scales/biases bf16 [N, K/group_size]; fp32 accumulation; bias may be NULL.
  * transpose must be 1 (the only form the reference uses,
  * `model/minimax h3/H3Common.swift:358-359`); transpose == 0 returns
- * MXQ_ERR_UNSUPPORTED. M <= MXQ_QMV_MAX_M runs the GEMV kernel, larger M an MFMA
- * kernel. M == 0 or N == 0 is a no-op.
- * For M > MXQ_QMV_MAX_M with K % 64 == 0 (and a tiled copy below 2 GiB) the call takes
+ * MXQ_ERR_UNSUPPORTED. M <= 8 runs the GEMV kernel; 9 <= M <= MXQ_QMV_MAX_M (K % 64 ==
+ * 0) the GEMV or an MFMA kernel, whichever an estimate from the weight's size and K
+ * finds faster; larger M an MFMA kernel. M == 0 or N == 0 is a no-op.
+ * When an MFMA kernel runs and K % 64 == 0 (and the tiled copy is below 2 GiB) the call takes
  * mxq_tiled_bytes(N, K, group_size, bits) bytes of stream-ordered workspace from a memory
  * pool the library owns (one per GPU, created on first use, kept until the process ends,
  * caching up to 256 MiB of freed workspace), tiles the weight into it, runs the tiled MFMA
- * kernel and frees the workspace on `stream`: for 2, 4, 6 and 8 bits the same result bits
- * as the in-place MFMA kernel (3- and 5-bit codes, whose in-place form is the GEMV
- * kernel, differ from it in the last bits). On a stream under graph capture, or where the
- * pool cannot supply the bytes, it runs the in-place kernel and allocates nothing. */
+ * kernel and frees the workspace on `stream`: the same result bits as the in-place MFMA
+ * kernel. On a stream under graph capture, or where the pool cannot supply the bytes, it
+ * runs the in-place kernel and allocates nothing. */
 int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq,
                          const void* scales, const void* biases, int64_t N, int transpose,
                          int group_size, int bits, const void* bias, void* y,
@@ -165,7 +166,7 @@ int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
             const void* biases, int64_t N, int group_size, int bits, const void* bias,
             void* y, mxq_stream stream);
 
-/* Small-M path only (split-K GEMV, no MFMA). 0 <= M <= MXQ_QMV_MAX_M. */
+/* Small-M path only (the GEMV kernels). 0 <= M <= MXQ_QMV_MAX_M. */
 int mxq_qmv(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void* scales,
             const void* biases, int64_t N, int group_size, int bits, const void* bias,
             void* y, mxq_stream stream);
@@ -192,8 +193,8 @@ int64_t mxq_tiled_bytes(int64_t N, int64_t K, int group_size, int bits);
 int mxq_tile(const uint32_t* wq, const void* scales, const void* biases, int64_t N, int64_t K,
              int group_size, int bits, void* tiled, mxq_stream stream);
 
-/* mxq_quantized_matmul on tiled weights: GEMV for M <= MXQ_QMV_MAX_M, else
- * the MFMA kernel. Same arithmetic and results as the MLX-layout paths. */
+/* mxq_quantized_matmul on tiled weights: the GEMV or the MFMA kernel by the same rule as
+ * mxq_quantized_matmul. Same arithmetic and results as the MLX-layout paths. */
 int mxq_quantized_matmul_tiled(const void* x, int64_t M, int64_t K, const void* tiled,
                                int64_t N, int group_size, int bits, const void* bias, void* y,
                                mxq_stream stream);

@@ -101,7 +101,8 @@ def test_matmul_caps_k(mxq_lib):
 
 def test_qmv_rejects_large_m(mxq_lib):
     L = mxq_lib
-    rc = L.mxq_qmv(_fake(), 9, 256, _fake(), _fake(), _fake(), 64, 64, 4, None, _fake(), None)
+    rc = L.mxq_qmv(_fake(), _lib.MXQ_QMV_MAX_M + 1, 256, _fake(), _fake(), _fake(), 64, 64, 4, None,
+                   _fake(), None)
     assert rc == _lib.MXQ_ERR_INVALID
 
 
@@ -136,7 +137,8 @@ def test_tiled_validation(mxq_lib):
     # the tiled buffer must be 16-byte aligned (the kernels read it with b128 loads)
     odd = ctypes.c_void_p(f.value + 4)
     assert L.mxq_qmm_tiled(f, 2, 128, odd, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_ALIGNMENT
-    assert L.mxq_qmv_tiled(f, 9, 128, f, 64, 64, 4, None, f, None) == _lib.MXQ_ERR_INVALID
+    assert L.mxq_qmv_tiled(f, _lib.MXQ_QMV_MAX_M + 1, 128, f, 64, 64, 4, None, f,
+                           None) == _lib.MXQ_ERR_INVALID
 
 
 def test_errors_are_thread_local(mxq_lib):

@@ -1,4 +1,4 @@
-"""mxq_quantized_matmul past the GEMV's range (M > 8) on the MLX layout: the weight is
+"""mxq_quantized_matmul past the GEMV's range (M > 32) on the MLX layout: the weight is
 tiled into a stream-ordered workspace from the library's pool and the tiled kernel runs.
 Checked through the C ABI against the in-place MFMA kernel (mxq_qmm) and the
 caller-workspace entry point (mxq_quantized_matmul_ws), bit for bit, and against the
@@ -71,7 +71,7 @@ def test_pooled_workspace_matches_in_place_kernel(dev, O, M, N, K, gs, bits):
                  f"pooled M={M} N={N} K={K} gs={gs} bits={bits}")
 
 
-@pytest.mark.parametrize("M,N,K,gs,bits", [(9, 512, 1024, 64, 6), (16, 2048, 2048, 64, 4),
+@pytest.mark.parametrize("M,N,K,gs,bits", [(33, 512, 1024, 64, 6), (48, 2048, 2048, 64, 4),
                                            (100, 700, 1536, 32, 8), (300, 1000, 2048, 128, 2),
                                            (640, 384, 4096, 64, 6)])
 def test_pooled_small_m_matches_in_place_kernel(dev, O, M, N, K, gs, bits):
@@ -92,16 +92,19 @@ def test_pooled_small_m_matches_in_place_kernel(dev, O, M, N, K, gs, bits):
                  f"pooled M={M} N={N} K={K} gs={gs} bits={bits}")
 
 
-@pytest.mark.parametrize("M,bits,gs", [(12, 3, 64), (1100, 5, 32), (300, 3, 128)])
+@pytest.mark.parametrize("M,bits,gs", [(40, 3, 64), (1100, 5, 32), (300, 3, 128)])
 def test_pooled_3_and_5_bit_codes(dev, O, M, bits, gs):
-    """3- and 5-bit codes: the pooled call runs the tiled MFMA kernel (the in-place form is
-    the GEMV kernel, whose sums differ in the last bits); checked against the oracle."""
+    """3- and 5-bit codes (runs of 32 codes are whole words, not 16-byte chunks): the
+    pooled call against the in-place kernel, bit for bit, and the oracle."""
     L = _lib.lib()
     N, K = 520, 1024
     host, d = _inputs(O, dev, M, N, K, gs, bits, seed=M + 7 * bits)
     y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    y_in = torch.empty_like(y)
     assert _plain(L, d, M, N, K, gs, bits, y) == _lib.MXQ_OK, L.mxq_last_error()
+    assert _in_place(L, d, M, N, K, gs, bits, y_in) == _lib.MXQ_OK
     torch.cuda.synchronize()
+    assert torch.equal(y, y_in), f"pooled vs in-place M={M} bits={bits} gs={gs}"
     x, wq, s, b, bias = host
     rows = np.unique(np.r_[np.arange(0, M, 11), M - 1])
     assert_tight(host_f32_of_bf16(y)[rows],

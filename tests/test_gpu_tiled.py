@@ -140,7 +140,7 @@ def test_tiled_qmm_shapes(dev, O, M, N, K):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("gs", GS)
-@pytest.mark.parametrize("M", [1, 2, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 16, 20, 32])
 def test_tiled_qmv_parity(dev, O, bits, gs, M):
     N, K = 200, 512
     x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 100 + gs + M + 1,
@@ -199,7 +199,8 @@ def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
     steps, gs = 128 groups split between batches), 3840 (the Gemma-4 logits K)."""
     for (M, N, K) in [(1, 200, 1024), (2, 200, 1024), (3, 200, 1024), (5, 200, 1024),
                       (8, 200, 1024), (2, 130, 192), (7, 130, 192), (1, 130, 320),
-                      (2, 200, 2688), (5, 70, 1856), (3, 300, 3840)]:
+                      (2, 200, 2688), (5, 70, 1856), (3, 300, 3840), (9, 200, 1024),
+                      (16, 130, 2688), (17, 200, 1024), (32, 96, 3840)]:
         if K % gs:
             continue
         x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 17 + gs + M,

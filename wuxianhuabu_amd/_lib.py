@@ -20,7 +20,7 @@ MXQ_FLOAT32 = 0
 MXQ_BFLOAT16 = 1
 MXQ_MODE_MINMAX = 0
 MXQ_MODE_MLX_EDGE = 1
-MXQ_QMV_MAX_M = 8
+MXQ_QMV_MAX_M = 32
 MXQ_ACT_NONE = 0
 MXQ_ACT_GELU_TANH = 1
 MXQ_ACT_SWIGLU = 2

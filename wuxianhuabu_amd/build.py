@@ -17,11 +17,12 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmxq.so")
 
-SOURCES = ["mxq_layout.hip", "mxq_qmv.hip", "mxq_qmm.hip", "mxq_qmm_tiled.hip",
+SOURCES = ["mxq_layout.hip", "mxq_qmv.hip", *[f"mxq_qmv_b{b}.hip" for b in (2, 3, 4, 5, 6, 8)],
+           "mxq_qmm.hip", "mxq_qmm_tiled.hip",
            *[f"mxq_qmm_tiled_b{b}.hip" for b in (2, 3, 4, 5, 6, 8)], "mxq_blockops.hip",
            "mxq_api.cpp", "mxq_safetensors.cpp"]
 HEADERS = ["mxq_device.hpp", "mxq_internal.hpp", "mxq_ring.hpp", "mxq_tiled.hpp",
-           "mxq_qmm_tiled_impl.hpp"]
+           "mxq_qmm_tiled_impl.hpp", "mxq_qmv_impl.hpp"]
 
 ARCH = "gfx950"
 COMMON = [

@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -308,7 +309,7 @@ int mxq_qmm(const void* x, int64_t M, int64_t K, const uint32_t* wq, const void*
   const auto* bs = static_cast<const uint16_t*>(bias);
   auto* yb = static_cast<uint16_t*>(y);
   if (!mxq::detail::qmm_supports_bits(bits)) {
-    // 3- and 5-bit codes: the GEMV kernel handles any M in blocks of 8 rows.
+    // a width the MFMA kernel does not take: the GEMV kernel handles any M in passes.
     return hip_status("quantized_matmul",
                       mxq::detail::launch_qmv(xb, static_cast<int>(M), static_cast<int>(K), wq,
                                               sc, bi, static_cast<int>(N), group_size, bits,
@@ -494,10 +495,35 @@ int mxq_qmv_tiled(const void* x, int64_t M, int64_t K, const void* tiled, int64_
                         static_cast<hipStream_t>(stream)));
 }
 
+}  // extern "C"
+
+namespace {
+// The GEMV or an MFMA kernel for M tokens. Up to 8 tokens the GEMV, one read of the
+// weight, always wins. From 9 to MXQ_QMV_MAX_M (K % 64 == 0) it runs one pass of 16 or 32
+// tokens, whose per-token work caps its rate (tiled layout: about 3.2 and 2.0 TB/s of
+// weight), while the MFMA kernel at these M is bound by its K loop: about 0.8 us per
+// 64-code step per round of 256 feature tiles. Measured on the tiled layout from
+// N x K = 2048 x 2048 to 262144 x 3840: the GEMV takes 0.26-0.6 of the MFMA kernel's time
+// for weights below about 120 MB at 32 tokens and below about 600 MB at 16. Both layouts
+// take the same decision, so a weight gives the same result bits tiled or not (the GEMV
+// applies the weights unrounded, the MFMA kernels as bf16).
+bool gemv_preferred(int64_t M, int64_t N, int64_t K, int gs, int bits) {
+  if (M <= 8) return true;
+  if (M > MXQ_QMV_MAX_M || K % 64 != 0 || gs <= 0) return false;
+  const double wbytes = static_cast<double>(N) * K * bits / 8.0 + 4.0 * N * (K / gs);
+  const double rounds = std::ceil(std::ceil(N / 256.0) / 256.0);
+  const double t_mfma = 0.8e-6 * (K / 64.0) * rounds;
+  const double t_gemv = wbytes / (M <= 16 ? 3.2e12 : 2.0e12);
+  return t_gemv <= t_mfma;
+}
+}  // namespace
+
+extern "C" {
+
 int mxq_quantized_matmul_tiled(const void* x, int64_t M, int64_t K, const void* tiled,
                                int64_t N, int group_size, int bits, const void* bias, void* y,
                                mxq_stream stream) {
-  if (M <= MXQ_QMV_MAX_M)
+  if (gemv_preferred(M, N, K, group_size, bits))
     return mxq_qmv_tiled(x, M, K, tiled, N, group_size, bits, bias, y, stream);
   return mxq_qmm_tiled(x, M, K, tiled, N, group_size, bits, bias, y, stream);
 }
@@ -505,8 +531,8 @@ int mxq_quantized_matmul_tiled(const void* x, int64_t M, int64_t K, const void* 
 }  // extern "C"
 
 namespace {
-// The MLX-layout operator without a workspace: the GEMV kernel up to MXQ_QMV_MAX_M
-// rows, the in-place MFMA kernel above. Allocates nothing.
+// The MLX-layout operator without a workspace: the GEMV kernel where gemv_preferred says
+// so, the in-place MFMA kernel otherwise. Allocates nothing.
 int matmul_in_place(const void* x, int64_t M, int64_t K, const uint32_t* wq,
                     const void* scales, const void* biases, int64_t N, int transpose,
                     int group_size, int bits, const void* bias, void* y, mxq_stream stream) {
@@ -514,7 +540,7 @@ int matmul_in_place(const void* x, int64_t M, int64_t K, const uint32_t* wq,
     return fail(MXQ_ERR_UNSUPPORTED,
                 "[quantized_matmul] transpose=false (x * W with W stored [K, N]) is not "
                 "implemented; the quantized linear layers use transpose=true.");
-  if (M <= MXQ_QMV_MAX_M)
+  if (gemv_preferred(M, N, K, group_size, bits))
     return mxq_qmv(x, M, K, wq, scales, biases, N, group_size, bits, bias, y, stream);
   return mxq_qmm(x, M, K, wq, scales, biases, N, group_size, bits, bias, y, stream);
 }
@@ -560,12 +586,12 @@ hipMemPool_t workspace_pool(hipStream_t stream) {
 }
 
 // Bytes of stream-ordered workspace a large-M mxq_quantized_matmul call tiles the weight
-// into, or 0 where it runs in place: any M past the GEMV's range, K % 64 == 0, a tiled
-// copy below 2 GiB. The tiled kernel takes 0.36-0.95 of the in-place kernel's time,
+// into, or 0 where it runs in place: K % 64 == 0 and a tiled copy below 2 GiB (the caller
+// takes this path only where the MFMA kernel beats the GEMV). The tiled kernel takes 0.36-0.95 of the in-place kernel's time,
 // tiling included, from M = 16 (M = 16 to 1024; N x K from 2048 x 2048 to 5376 x 21504,
-// 6-bit), and covers the 3- and 5-bit codes whose in-place form is the GEMV kernel.
+// 6-bit).
 int64_t pooled_workspace_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits) {
-  if (M <= MXQ_QMV_MAX_M || M > INT32_MAX || N <= 0 || N > INT32_MAX || K <= 0 ||
+  if (M <= 0 || M > INT32_MAX || N <= 0 || N > INT32_MAX || K <= 0 ||
       K % 64 != 0 || K > kMaxK || check_bits_gs("quantized_matmul", bits, gs, K) != MXQ_OK)
     return 0;
   const int64_t t = mxq::tiled::total_bytes(N, K, gs, bits);
@@ -607,11 +633,10 @@ int mxq_quantized_matmul(const void* x, int64_t M, int64_t K, const uint32_t* wq
                          int group_size, int bits, const void* bias, void* y,
                          mxq_stream stream) {
   // Past the GEMV's range: the weight is tiled into a stream-ordered workspace and the
-  // tiled kernel runs (for 2, 4, 6 and 8 bits the same result bits as the in-place
-  // kernel; about 1.7x faster at M = 14400, K = 4096, N = 16384 and up to 2.8x at a few
-  // hundred tokens). Invalid arguments are refused before anything is allocated; where no
+  // tiled kernel runs (the same result bits as the in-place kernel; about 1.7x faster at
+  // M = 14400, K = 4096, N = 16384 and up to 2.8x at a few hundred tokens). Invalid arguments are refused before anything is allocated; where no
   // workspace can be had, the in-place kernel runs.
-  if (transpose == 1 && M > MXQ_QMV_MAX_M) {
+  if (transpose == 1 && !gemv_preferred(M, N, K, group_size, bits)) {
     const int64_t need = pooled_workspace_bytes(M, N, K, group_size, bits);
     if (need > 0) {
       int rc = check_matmul("quantized_matmul", x, M, K, wq, scales, biases, N, group_size,

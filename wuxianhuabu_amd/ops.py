@@ -170,7 +170,7 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
                      bias=None, path="auto"):
     """y [..., N] = x [..., K] @ dequantized(w)^T (+ bias), bf16 in/out, fp32 accumulate.
 
-    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv" to force a kernel.
+    path: "auto" (GEMV for M <= MXQ_QMV_MAX_M = 32, MFMA above), "qmm" or "qmv" to force a kernel.
     With "auto" and many tokens (mxq_quantized_matmul_workspace_size > 0) the weight is
     tiled into a temporary buffer first and the tiled MFMA kernel runs: the same
     result bits, in less time.
@@ -326,7 +326,7 @@ class LoraAdapters:
 def tiled_matmul(x, tw, *, bias=None, path="auto", activation=None, lora=None):
     """quantized_matmul(x, w, scales, biases, transpose=True, ...) on a TiledWeight.
 
-    path: "auto" (GEMV for M <= 8, MFMA above), "qmm" or "qmv".
+    path: "auto" (GEMV for M <= MXQ_QMV_MAX_M = 32, MFMA above), "qmm" or "qmv".
     activation (fused into the MFMA kernel's epilogue, applied in fp32 before the
     one bf16 rounding; any M): None, "gelu_tanh" (geluApprox between the LTX
     feed-forward projections), or "swiglu" (silu(gate) * up of a weight tiled
