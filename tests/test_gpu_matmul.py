@@ -63,6 +63,20 @@ def test_qmv_parity(dev, O, bits, gs, M):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", [(1, 100, 2048), (5, 200, 2176), (32, 72, 4224)])
+def test_qmv_eight_wave_split(dev, O, bits, gs, M, N, K):
+    """Fewer than 512 workgroups and K >= 2048: the GEMV splits K over 8 waves per
+    workgroup instead of 4 (K = 2176 and 4224 are 34 and 66 steps of 64 codes, which do
+    not divide evenly over the waves)."""
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 31 + gs + M + K,
+                                  with_bias=(M != 5))
+    y = run(dev, x, wq, s, b, bias, gs, bits, path="qmv")
+    ref = O.qmm_f64(x, wq, s, b, gs, bits, bias=bias)
+    assert_tight(y, ref, f"qmv 8 waves bits={bits} gs={gs} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("M", [1, 2, 5, 8])
 @pytest.mark.parametrize("N,K", [(96, 96), (40, 544), (17000, 160)])
 def test_qmv_k_odd_multiple_of_32(dev, O, bits, M, N, K):

@@ -154,6 +154,19 @@ def test_tiled_qmv_parity(dev, O, bits, gs, M):
 
 @pytest.mark.parametrize("bits", BITS)
 @pytest.mark.parametrize("gs", GS)
+@pytest.mark.parametrize("M,N,K", [(1, 100, 2048), (5, 200, 2176), (32, 72, 4224)])
+def test_tiled_qmv_eight_wave_split(dev, O, bits, gs, M, N, K):
+    """The tiled GEMV with K split over 8 waves (fewer than 512 workgroups, K >= 2048)."""
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 37 + gs + M + K,
+                                  with_bias=(M != 5))
+    tw = _tile(dev, wq, s, b, gs, bits)
+    y = host_f32_of_bf16(_tiled_run(dev, x, tw, bias, path="qmv"))
+    ref = O.qmm_f64(x, wq, s, b, gs, bits, bias=bias)
+    assert_tight(y, ref, f"tiled qmv 8 waves bits={bits} gs={gs} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("gs", GS)
 def test_workspace_matmul_bit_identical(dev, O, bits, gs):
     """quantized_matmul(path="auto") at M >= 1024 tiles the MLX-layout weight into a
     workspace and runs the tiled kernel: the same bits as the MLX-layout MFMA kernel.
@@ -196,11 +209,14 @@ def test_mlx_qmv_bit_identical_to_tiled_qmv(dev, O, bits, gs):
     coalesced loads then straddle row ends. The MLX form loads each batch's scales and
     biases as one window per row: K = 320 (5 groups of 64 per row, so the window's
     alignment differs between rows), 2688 and 1856 (waves whose batches start at odd
-    steps, gs = 128 groups split between batches), 3840 (the Gemma-4 logits K)."""
+    steps, gs = 128 groups split between batches), 3840 (the Gemma-4 logits K). 16-token
+    passes (M = 12, 16) at N = 16384 run 4 waves per workgroup over long K spans, where
+    even widths take 2-step batches."""
     for (M, N, K) in [(1, 200, 1024), (2, 200, 1024), (3, 200, 1024), (5, 200, 1024),
                       (8, 200, 1024), (2, 130, 192), (7, 130, 192), (1, 130, 320),
                       (2, 200, 2688), (5, 70, 1856), (3, 300, 3840), (9, 200, 1024),
-                      (16, 130, 2688), (17, 200, 1024), (32, 96, 3840)]:
+                      (16, 130, 2688), (17, 200, 1024), (32, 96, 3840),
+                      (16, 16384, 2048), (12, 16384, 2560)]:
         if K % gs:
             continue
         x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=bits * 17 + gs + M,

@@ -286,11 +286,11 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // LDS region, and lane (l32, g2) reads back the BITS words of codes
 // [64k + 32 g2, +32) of its row l32 (a run of 32 codes is BITS whole words);
 // it loads that row's scale and bias of step k's group(s) itself. Everything
-// else is shared. gshift = log2(gs / 64) for gs >= 64. With batches of 4 steps, a lane
-// loads its row's scales (and biases) of the whole batch at once: a dword-aligned window
-// of 12 bytes (16 for gs = 32) holding the batch's groups, split where used. A row's
-// scales for all of K lie in one or two 128-byte lines, which one 2-byte load per step
-// asked L2 for once per step.
+// else is shared. gshift = log2(gs / 64) for gs >= 64. With batches of 2 or 4 steps, a
+// lane loads its row's scales (and biases) of the whole batch at once: a dword-aligned
+// window holding the batch's groups (12 bytes for 4 steps, 16 for 4 steps at gs = 32,
+// 8 for 2 steps), split where used. A row's scales for all of K lie in one or two
+// 128-byte lines, which one 2-byte load per step asked L2 for once per step.
 template <int BITS, int MT, int GP, int NH, int WPB, int SPW, bool MLX>
 __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     const uint16_t* __restrict__ x, int M, int K, const uint8_t* __restrict__ tw, int N,
@@ -319,6 +319,8 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   constexpr int NCL = 32 * CPR / 64;           // coalesced 16-byte loads per lane per half
   constexpr int RSTR = CPR * 16 + 16;          // staged row stride
   static_assert(!MLX || (SPW * BITS) % 4 == 0, "whole loads of 64 lanes per batch");
+  // MLX: batches of 2 or 4 steps load their scales and biases as whole windows
+  constexpr bool kWin = MLX && (SPW == 2 || SPW == 4);
   __shared__ __attribute__((aligned(16))) uint8_t wl_all[WPB][MLX ? NH * 32 * RSTR : 16];
 
   // Naming an AGPR keeps the MFMA results in AGPRs. A kernel that names none may
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           }
         }
         if constexpr (MLX) {
-          if constexpr (SPW == 4) {
+          if constexpr (kWin) {
             // whole-batch windows, below
           } else if constexpr (GP == 2) {  // groups 2k and 2k + 1
             const int ss = __builtin_amdgcn_readfirstlane(kj * 4);
@@ -541,6 +543,17 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           B.sb[0][nb][0] = sv.x; B.sb[1][nb][0] = sv.y; B.sb[2][nb][0] = sv.z;
           B.sb[0][nb][1] = bv.x; B.sb[1][nb][1] = bv.y; B.sb[2][nb][1] = bv.z;
         }
+      }
+    } else if constexpr (kWin) {
+      // 2-step batches, the same windows: GP == 2, two dwords; GP == 1, two dwords from
+      // the even halfword at or below group b0 >> gshift
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) {
+        const int a = GP == 2 ? svo[nb] + 4 * b0 : (((svo[nb] >> 1) + (b0 >> gshift)) & ~1) * 2;
+        const v2u_t sv = __builtin_amdgcn_raw_buffer_load_b64(srs, a, 0, kWeightAux);
+        const v2u_t bv = __builtin_amdgcn_raw_buffer_load_b64(brs, a, 0, kWeightAux);
+        B.sb[0][nb][0] = sv.x; B.sb[1][nb][0] = sv.y;
+        B.sb[0][nb][1] = bv.x; B.sb[1][nb][1] = bv.y;
       }
     }
   };
@@ -639,7 +652,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
           float sc, bi;
           if constexpr (MLX) {
             uint32_t sv = B.sb[j][nb][0], bv2 = B.sb[j][nb][1];
-            if constexpr (GP == 1 && SPW == 4) {
+            if constexpr (GP == 1 && kWin) {
               // halfword h of the window: group (b0 + j) >> gshift, counted from the
               // window's first (even) halfword
               const int hw0 = (svo[nb] >> 1) + (b0 >> gshift);
@@ -647,10 +660,17 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
               const int d = h >> 1;
               // values, not lvalues: a choice between elements would index the batch
               // at run time and move it to scratch memory
-              const uint32_t s0 = B.sb[0][nb][0], s1 = B.sb[1][nb][0], s2 = B.sb[2][nb][0];
-              const uint32_t c0 = B.sb[0][nb][1], c1 = B.sb[1][nb][1], c2 = B.sb[2][nb][1];
-              const uint32_t ws = d == 0 ? s0 : d == 1 ? s1 : s2;
-              const uint32_t wb = d == 0 ? c0 : d == 1 ? c1 : c2;
+              const uint32_t s0 = B.sb[0][nb][0], s1 = B.sb[1][nb][0];
+              const uint32_t c0 = B.sb[0][nb][1], c1 = B.sb[1][nb][1];
+              uint32_t ws, wb;
+              if constexpr (SPW == 4) {
+                const uint32_t s2 = B.sb[2][nb][0], c2 = B.sb[2][nb][1];
+                ws = d == 0 ? s0 : d == 1 ? s1 : s2;
+                wb = d == 0 ? c0 : d == 1 ? c1 : c2;
+              } else {
+                ws = d == 0 ? s0 : s1;
+                wb = d == 0 ? c0 : c1;
+              }
               sv = (h & 1) ? ws >> 16 : ws;
               bv2 = (h & 1) ? wb >> 16 : wb;
             }
@@ -775,11 +795,13 @@ hipError_t run_qmv_mlx(const uint16_t* x, int M, int K, const uint32_t* wq, cons
   // batches of 4 steps: a batch reads 4 x 8 * BITS contiguous bytes of each row (192 B
   // at 6 bits), so fewer of a row's 128-byte lines are split between batches
   // (M = 2, N = 24576: 31.4 us against 32.8 us with 2 steps; 8 or 16 steps, two
-  // record halves per workgroup or 2 waves per workgroup were slower)
-#ifndef MXQ_QMV_MLX_SPW
-#define MXQ_QMV_MLX_SPW 4
-#endif
-  constexpr int NH = 1, SPW = MXQ_QMV_MLX_SPW;
+  // record halves per workgroup or 2 waves per workgroup were slower). 16-token passes
+  // of even code widths take batches of 2: two 4-step batches of 16 tokens' activations
+  // (64 VGPRs) and codes held 273-308 VGPRs per lane at 4 waves, one wave per SIMD, and
+  // spilled at 8 waves; with 2 steps, 184-204 and no spills (6-bit, K = 4096: N = 24576
+  // 48.8 -> 38.5 us, N = 7168 19.5 -> 13.5 us; K = 21504, N = 5376: 74.8 -> 52.6 us).
+  // 8-token passes stay at 4 steps (2 steps: 38.7 -> 45.5 us at K = 21504).
+  constexpr int NH = 1, SPW = (MT >= 16 && BITS % 2 == 0) ? 2 : 4;
   dim3 grid((N + 63) / 64 * (2 / NH), (M + MT - 1) / MT);
 #define MXQ_QMV_LAUNCH(G, W, GSH)                                              \
   qmv_tiled_kernel<BITS, MT, G, NH, W, SPW, true><<<grid, 64 * W, 0, s>>>(     \
