@@ -238,8 +238,8 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 // ---------------------------------------------------------------------------
 // GEMV on the tiled layout (mxq_tiled.hpp). HBM-bound, so the design goal is
 // bytes in flight with as little VALU work per byte as possible: one
-// workgroup of a few waves per 32-row record half; the waves split the K steps
-// into contiguous spans (a row block's records are contiguous in HBM). Each
+// workgroup of a few waves per 32-row record half; the waves take the K steps
+// in chunks of 4, round robin. Each
 // wave works in batches of up to SPW steps, with two register sets: while
 // batch b computes, every load of batch b+1 (its activation slice, MT rows x
 // SPW steps x 128 B, and its weight units) is in flight. Computing a batch
@@ -266,6 +266,11 @@ hipError_t pick_mt(const uint16_t* x, int M, int K, const uint32_t* wq, const ui
 // (25.6 us; 38.1 with non-temporal loads). The activations, which every workgroup
 // reads, keep the default too.
 constexpr int kTiledWeightAux = 2;
+// K steps per chunk of the waves' round-robin split. Against one contiguous K quarter
+// per wave (6-bit, same box): K = 4096, N = 24576, tiled 14.82 -> 14.58 us at M = 2
+// (15.9 -> 14.8 at M = 3), MLX layout 21.5 -> 20.3 us; K = 21504, N = 5376, M = 1, MLX
+// layout 31.9 -> 28.0 us; 8 and 16 tokens within 1 %.
+constexpr int kQmvChunk = 4;
 typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
 typedef uint32_t v3u_t __attribute__((ext_vector_type(3)));
 typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
@@ -402,8 +407,17 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
     xa[e] = (l32 < MT && (GP == 1 || g2 == e) ? xw + l32 * (SPW * 128) : zero_chunk[wave]) +
             g2 * 64;
 
-  const int per = (nk + WPB - 1) / WPB;
-  const int k_begin = wave * per, k_end = min(nk, k_begin + per);
+  // The waves take the K steps in chunks of kQmvChunk, round robin: wave w sums chunks
+  // w, w + WPB, w + 2 WPB, ... in step order, whatever its batch size, so both layouts
+  // (1-step batches tiled, 2 or 4 steps over the MLX layout) give the same bits. At any
+  // time a workgroup's waves read neighbouring chunks of its rows.
+  static_assert(kQmvChunk % SPW == 0, "batches tile the chunks");
+  const int k_begin = wave * kQmvChunk, k_end = nk;
+  // the batch after the one at b0: the next SPW steps of its chunk, else the wave's next chunk
+  auto next_batch = [&](int b) {
+    const int n = b + SPW;
+    return n % kQmvChunk == 0 ? n + kQmvChunk * (WPB - 1) : n;
+  };
   // pair_at's constants, in VGPRs
   uint32_t kPairMask = ((1u << BITS) - 1u) * 0x10001u, kMagic = 0x43004300u;
   asm volatile("" : "+v"(kPairMask), "+v"(kMagic));
@@ -700,20 +714,22 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   if (b0 < k_end) {
     load(ba, b0);
     for (;;) {
-      if (b0 + SPW >= k_end) {
+      int b1 = next_batch(b0);
+      if (b1 >= k_end) {
         consume(Part{}, ba, b0);
         break;
       }
-      load(bb, b0 + SPW);
+      load(bb, b1);
       consume(Whole{}, ba, b0);
-      b0 += SPW;
-      if (b0 + SPW >= k_end) {
+      b0 = b1;
+      b1 = next_batch(b0);
+      if (b1 >= k_end) {
         consume(Part{}, bb, b0);
         break;
       }
-      load(ba, b0 + SPW);
+      load(ba, b1);
       consume(Whole{}, bb, b0);
-      b0 += SPW;
+      b0 = b1;
     }
   }
 
@@ -748,7 +764,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 // rotated copies (median of 7 x 50 launches): 1-step batches 14.4 us at M = 2 (14.4 at
 // M = 1, 15.4 at M = 8); 2-step 14.9 (14.6, 17.8); 3-step 16.1; 4-step 15.7; 8 waves
 // with 2-step batches 15.1 (21.4 at M = 8), with 1-step 15.2. Results are the same bits
-// for every batch size (each wave sums its K span in step order).
+// for every batch size (each wave sums its chunks in step order).
 #ifndef MXQ_QMV_WAVES
 #define MXQ_QMV_WAVES 4
 #endif
@@ -758,7 +774,7 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
 constexpr int kTiledNH = 1, kTiledWaves = MXQ_QMV_WAVES, kTiledSPW = MXQ_QMV_SPW;
 
 // Waves per workgroup: 8 where fewer than 512 workgroups would run and K holds 32 steps
-// or more (each wave keeps a span of at least 4), else 4. A small grid then keeps more
+// or more (each wave keeps at least one whole chunk), else 4. A small grid then keeps more
 // loads in flight (M = 1, N = 5376, K = 21504: 25.3 against 36.7 us; 16 waves, 21.8 us,
 // do not fit the MLX layout's staging in LDS); large grids are faster with 4 (N = 24576:
 // 16.7 against 18.8 us). The tiled and MLX-layout launches use the same rule, so they split
