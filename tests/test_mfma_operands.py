@@ -9,6 +9,13 @@ This test disassembles the gfx950 code objects of the library (the
 `.hip_fatbin` section: one clang offload bundle per translation unit) and checks
 all MFMAs. It runs on the CPU, on the library built in this tree.
 
+Wait states: an MFMA that reads a VGPR needs two wait states (instructions, an
+`s_nop n` counting n + 1) after the VALU instruction that wrote it. The compiler
+counts them for the instructions it generates, not for inline assembly: a code-pair
+unpack written as inline assembly reached the GEMV's MFMAs one instruction later in
+some schedules, and the 5-bit GEMV then gave wrong sums in builds of equivalent
+source. Every MFMA in the library is checked within its basic block.
+
 Scratch: a choice between elements of a register array made at run time (e.g.
 `c ? a[0] : a[1]` on lvalues, a select between two addresses) moves the array to
 per-lane scratch memory. The MLX-layout GEMV once did so with its batch of
@@ -174,3 +181,83 @@ def test_library_kernels_keep_no_arrays_in_scratch():
             bad += scratch_arrays(notes)
     assert kernels > 100, f"only {kernels} kernels found"
     assert not bad, f"{len(bad)} kernels keep arrays in scratch memory, e.g. {bad[:3]}"
+
+
+INSN = re.compile(r"^\s+(\S+)\s*(.*?)\s*//\s*([0-9A-Fa-f]+):")
+FUNC = re.compile(r"^([0-9a-f]+) <(\S+)>:")
+BRANCH = re.compile(r"s_c?branch\S*.*<(\S+)\+0x([0-9a-f]+)>")
+
+
+def _vregs(tok):
+    m = re.match(r"v\[(\d+):(\d+)\]$", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def close_valu_mfma(text, need=2):
+    """(MFMA count, MFMAs reading an A or B VGPR written by a VALU instruction fewer than
+    `need` wait states earlier in the same basic block) of `llvm-objdump -d` output."""
+    funcs = {m.group(2): int(m.group(1), 16) for m in FUNC.finditer(text)}
+    starts = {funcs[m.group(1)] + int(m.group(2), 16) for m in BRANCH.finditer(text)
+              if m.group(1) in funcs}
+    count, bad, last, pos = 0, [], {}, 0
+    for line in text.splitlines():
+        if FUNC.match(line):
+            last = {}
+            continue
+        m = INSN.match(line)
+        if not m:
+            continue
+        op, ops = m.group(1), [t.strip() for t in m.group(2).split(",")]
+        if int(m.group(3), 16) in starts:
+            last = {}
+        if op.startswith("v_mfma"):
+            count += 1
+            for r in _vregs(ops[1]) | _vregs(ops[2]):
+                if r in last and pos - last[r] - 1 < need:
+                    bad.append(f"{op} {m.group(2)} (v{r} written {pos - last[r] - 1} states before)")
+                    break
+        nop = re.match(r"s_nop\s+(\d+)", f"{op} {m.group(2)}")
+        if op.startswith("v_") and not op.startswith(("v_mfma", "v_cmp")) and ops[0]:
+            for r in _vregs(ops[0]):
+                last[r] = pos
+        if op.startswith(("s_branch", "s_cbranch", "s_setpc")):
+            last = {}
+        pos += int(nop.group(1)) + 1 if nop else 1
+    return count, bad
+
+
+def test_wait_state_detector():
+    text = """0000000000001000 <k>:
+\tv_and_or_b32 v95, v95, v27, v31   // 000000001000: 0
+\tv_add_u32_e32 v12, s2, v34        // 000000001008: 0
+\tv_mfma_f32_32x32x16_bf16 a[0:15], v[100:103], v[92:95], 0   // 000000001010: 0
+\tv_and_or_b32 v91, v91, v27, v31   // 000000001018: 0
+\ts_nop 1                           // 000000001020: 0
+\tv_mfma_f32_32x32x16_bf16 a[0:15], v[100:103], v[88:91], a[0:15]   // 000000001024: 0
+\tv_and_or_b32 v87, v87, v27, v31   // 00000000102C: 0
+\ts_cbranch_scc1 1                  // 000000001034: 0 <k+0x3c>
+\ts_nop 0                           // 000000001038: 0
+\tv_mfma_f32_32x32x16_bf16 a[0:15], v[100:103], v[84:87], a[0:15]   // 00000000103C: 0
+"""
+    count, bad = close_valu_mfma(text)
+    assert count == 3
+    assert len(bad) == 1 and "v95" in bad[0]  # one VALU between; s_nop 1 is two states
+
+
+def test_library_mfmas_wait_for_their_valu_operands():
+    objdump = _tool("llvm-objdump")
+    if not objdump:
+        pytest.skip("llvm-objdump not available")
+    total, bad = 0, []
+    with tempfile.TemporaryDirectory() as td:
+        for path in _library_objects(td):
+            out = subprocess.run([objdump, "-d", "--no-show-raw-insn", path], check=True,
+                                 capture_output=True, text=True).stdout
+            c, b = close_valu_mfma(out)
+            total += c
+            bad += b
+    assert total > 1000, f"only {total} MFMA instructions found"
+    assert not bad, f"{len(bad)} MFMAs read a VGPR too soon after its VALU write, e.g. {bad[:3]}"

@@ -76,26 +76,26 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[NW], int i) {
 // (128 + q_i, 128 + q_{i+1}), for bits <= 7: their 2*BITS-bit field F is spread
 // so the second code lands at bit 16, then 0x43 supplies each half's exponent
 // (0x4300 | q is exactly 128 + q for q < 128).
-// Written as three VALU instructions (bfe, lshl_or, and_or; four when the field
-// straddles two words): left to itself the compiler splits the field into its
-// two codes and spends four or five. `mask` and `magic` are the constants
-// MASK | MASK << 16 and 0x43004300 held in VGPRs (VOP3 takes no literals here).
+// Three VALU instructions (bfe, lshl_or, and_or; four when the field straddles two
+// words). `mask` and `magic` are the constants MASK | MASK << 16 and 0x43004300 held
+// in VGPRs whose values the compiler does not know (VOP3 takes no literals here):
+// knowing the mask, it splits the field into its two codes and spends four or five.
+// Plain code, not inline assembly: the result feeds the MFMAs, and the compiler
+// places the wait states a VALU result needs before an MFMA reads it only for
+// instructions it generated itself. Written as inline assembly, the pair reached
+// the MFMA one instruction later in some schedules and the MFMA read a stale
+// register (wrong sums, depending on the build).
 template <int BITS, int NW>
 __device__ __forceinline__ uint32_t pair_at(const uint32_t (&w)[NW], int i, uint32_t mask,
                                             uint32_t magic) {
   static_assert(BITS <= 7, "0x4300 | q needs q < 128");
   const int p = i * BITS;
   const int wd = p >> 5, off = p & 31;
-  uint32_t f, r;
-  if (off + 2 * BITS <= 32) {
-    asm("v_bfe_u32 %0, %1, %2, %3" : "=v"(f) : "v"(w[wd]), "n"(off), "n"(2 * BITS));
-  } else {
-    const uint32_t a = __builtin_amdgcn_alignbit(w[wd + 1], w[wd], off);
-    asm("v_bfe_u32 %0, %1, 0, %2" : "=v"(f) : "v"(a), "n"(2 * BITS));
-  }
-  asm("v_lshl_or_b32 %0, %1, %2, %1\n\tv_and_or_b32 %0, %0, %3, %4"
-      : "=&v"(r) : "v"(f), "n"(16 - BITS), "v"(mask), "v"(magic));
-  return r;
+  constexpr uint32_t FMASK = (1u << (2 * BITS)) - 1u;
+  const uint32_t f = off + 2 * BITS <= 32
+                         ? (w[wd] >> off) & FMASK
+                         : __builtin_amdgcn_alignbit(w[wd + 1], w[wd], off) & FMASK;
+  return (((f << (16 - BITS)) | f) & mask) | magic;
 }
 
 template <int BITS, int NCODES, int NW, int I = 0>
