@@ -358,6 +358,12 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
   // packed as (row within the half) | (chunk << 8), unpacked where used
   int tcq[MLX ? NCL : 1];
   int rows = 0, rowb = 0, step_bytes = 0;
+  // MLX, one group per step or fewer: the block's last scale and bias (halfword s_last).
+  // When rows * G is odd it shares its dword with the two bytes past the descriptor's
+  // end, and the range check returns that whole dword as zero to the window loads; it is
+  // loaded once on its own and used in place of the window's value.
+  int s_last = -1;
+  uint32_t s_tail = 0, b_tail = 0;
   if constexpr (MLX) {
     rowb = K / 8 * BITS;                                // bytes per weight row
     const int G = GP == 2 ? K >> 5 : K >> (6 + gshift);  // groups per row
@@ -367,6 +373,11 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
                           static_cast<uint32_t>(rows) * rowb);
     srs = ring::make_rsrc(scs + static_cast<int64_t>(r0) * G, static_cast<uint32_t>(rows) * G * 2);
     brs = ring::make_rsrc(bis + static_cast<int64_t>(r0) * G, static_cast<uint32_t>(rows) * G * 2);
+    if constexpr (GP == 1 && kWin) {
+      s_last = rows * G - 1;
+      s_tail = __builtin_amdgcn_raw_buffer_load_b16(srs, s_last * 2, 0, 0);
+      b_tail = __builtin_amdgcn_raw_buffer_load_b16(brs, s_last * 2, 0, 0);
+    }
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb) {
       const int r = min((h0 + nb) * 32 + l32, rows - 1);  // rows past N repeat the last one
@@ -687,6 +698,10 @@ __global__ __launch_bounds__(64 * WPB) void qmv_tiled_kernel(
               }
               sv = (h & 1) ? ws >> 16 : ws;
               bv2 = (h & 1) ? wb >> 16 : wb;
+              if ((hw0 & ~1) + h == s_last) {
+                sv = s_tail;
+                bv2 = b_tail;
+              }
             }
             sc = __uint_as_float(e ? sv & 0xFFFF0000u : sv << 16);
             bi = __uint_as_float(e ? bv2 & 0xFFFF0000u : bv2 << 16);
