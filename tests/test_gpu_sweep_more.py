@@ -7,7 +7,8 @@ dequantizer and the fused epilogues, against the oracle.
   kernels), whichever kernel the shape selects;
 - `quantized` (both quantizers, fp32 and bf16 scales) and `dequantized`, 16 cases each,
   bit for bit;
-- the tiled MFMA kernel with GELU-tanh or SwiGLU fused, 12 cases, on sampled rows.
+- the tiled MFMA kernel with GELU-tanh or SwiGLU fused, 12 cases, and with LoRA adapters
+  (one or two, ranks 1-39, each activation), 8 cases, on sampled rows.
 """
 import ctypes
 
@@ -142,3 +143,39 @@ def test_fused_epilogue_random_geometry(dev, O, M, N, K, gs, bits, act):
     assert_tight(got, f(pre), f"{act} M={M} N={N} K={K} gs={gs} bits={bits}")
     exact = f(O.qmm_f64(x, wq, s, b, gs, bits, bias=bias, rows=rows))
     assert spec_metric(got, exact) <= 2e-2
+
+
+def _lora_cases(n=8, seed=17):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        bits = int(rng.choice([2, 3, 4, 5, 6, 8]))
+        gs = int(rng.choice([32, 64, 128]))
+        K = int(rng.integers(1, 2048 // 128 + 1)) * 128
+        ranks = [int(r) for r in rng.integers(1, 40, size=int(rng.integers(1, 3)))]
+        act = [None, "gelu_tanh", "swiglu"][i % 3]
+        out.append((int(rng.integers(1, 900)), int(rng.integers(1, 300)) * 2, K, gs, bits, act,
+                    ranks))
+    return out
+
+
+LORA = _lora_cases()
+
+
+@pytest.mark.parametrize("M,N,K,gs,bits,act,ranks", LORA,
+                         ids=[f"M{c[0]}-N{c[1]}-K{c[2]}-g{c[3]}-b{c[4]}-{c[5]}" for c in LORA])
+def test_lora_random_geometry(dev, O, M, N, K, gs, bits, act, ranks):
+    from tests.test_gpu_lora import _ACT, _adapters
+    x, wq, s, b, bias = make_case(O, M, N, K, gs, bits, seed=M + N + K, with_bias=True)
+    tw = mx.tile(dev_words(wq, dev), dev_bf16(s, dev), dev_bf16(b, dev), gs, bits,
+                 swiglu=act == "swiglu")
+    refs = _adapters(dev, K, N, ranks, seed=M + K)
+    lora = mx.LoraAdapters(refs)
+    xd = dev_bf16(x, dev)
+    y = mx.tiled_matmul(xd, tw, bias=dev_bf16(bias, dev), activation=act, lora=lora)
+    rows = np.unique(np.r_[np.linspace(0, M - 1, min(M, 12)).astype(int), M - 1])
+    got = host_f32_of_bf16(y)[rows]
+    xa = host_f32_of_bf16(lora.xa(xd))[rows]
+    base = O.qmm_f64_bf16w(x, wq, s, b, gs, bits, bias=bias, rows=rows)
+    assert_tight(got, _ACT[act](O, base + xa @ host_f32_of_bf16(lora.bt).T),
+                 f"lora M={M} N={N} K={K} gs={gs} bits={bits} act={act} ranks={ranks}")
