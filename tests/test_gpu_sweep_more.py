@@ -113,13 +113,14 @@ def test_quantize_dequantize_random_geometry(dev, O, N, bits, gs, K, mode):
 
 
 def _fused_cases(n=12, seed=13):
+    """K a multiple of 64 and of the group size (the tiled layout's steps)."""
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
-        bits, gs, K = _draw(rng, 2048)
-        K = max(64, K // 64 * 64) if K % 64 else K
-        if K % gs:
-            K = gs * max(1, K // gs) if gs <= 64 else 128 * max(1, K // 128)
+        bits = int(rng.choice([2, 3, 4, 5, 6, 8]))
+        gs = int(rng.choice([32, 64, 128]))
+        step = max(64, gs)
+        K = int(rng.integers(1, 2048 // step + 1)) * step
         out.append((int(rng.integers(1, 601)), int(rng.integers(1, 400)) * 2, K, gs, bits,
                     "gelu_tanh" if i % 2 == 0 else "swiglu"))
     return out
