@@ -93,3 +93,34 @@ def test_blockops_errors(dev):
     with pytest.raises(ValueError, match=r"rot"):
         mx.fused_rmsnorm_rope(x.reshape(1, 4, 1, 8), x[0], torch.zeros(4, 5, device=dev),
                               torch.zeros(4, 5, device=dev), 10)
+
+
+def _sweep(n, seed):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 400)), int(rng.integers(1, 6000)), int(rng.integers(1, 5)))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("S,hidden,rows", _sweep(10, 23))
+def test_norm_modscale_and_mod_gate_random_geometry(dev, O, S, hidden, rows):
+    """Seeded random token counts, widths (odd ones included) and modulation rows, with
+    runs of rows mapped to random modulation rows."""
+    rng = np.random.default_rng(S * 7 + hidden)
+    x = _rand(O, rng, (S, hidden), 2.0)
+    w = _rand(O, rng, hidden, 0.3, 1.0)
+    sh = _rand(O, rng, (rows, hidden), 0.5)
+    sc = _rand(O, rng, (rows, hidden), 0.5)
+    cut = int(rng.integers(0, S + 1))
+    runs = [(0, cut, int(rng.integers(0, rows))), (cut, S, int(rng.integers(0, rows)))]
+    rm = mx.build_row_mod_map(S, [r for r in runs if r[1] > r[0]], device=dev)
+    m = rm.view(torch.int32).cpu().numpy()
+    y = mx.fused_norm_modscale(dev_bf16(x, dev), dev_bf16(w, dev), dev_bf16(sh, dev),
+                               dev_bf16(sc, dev), rm, eps=1e-6)
+    carry = O.rmsnorm_bf16(x, w, 1e-6) * (O.bf16_to_f32(sc)[m] + 1)
+    _close(host_f32_of_bf16(y), O.norm_modscale_f64(x, w, sh, sc, m, 1e-6), carry,
+           f"norm_modscale S={S} hidden={hidden} rows={rows}")
+    o = _rand(O, rng, (S, hidden))
+    g = _rand(O, rng, (rows, hidden), 0.5)
+    y = mx.fused_mod_gate(dev_bf16(x, dev), dev_bf16(g, dev), dev_bf16(o, dev), rm)
+    ref = O.mod_gate_f64(x, o, g, m)
+    _close(host_f32_of_bf16(y), ref, 0 * ref, f"mod_gate S={S} hidden={hidden} rows={rows}")
